@@ -1,0 +1,179 @@
+"""hy3_amd -- MI355X (gfx950) Hy3 MoE FFN block: host-side binding.
+
+The product is libhy3x.so (HIP, C ABI in include/hy3x_moe.h). This module
+loads it with ctypes and wraps the layer object. Device memory and streams
+are passed as raw pointers (torch is used only as a convenient allocator by
+the tests and the benchmark). There is no CPU fallback: if the library is not
+built, every entry point raises.
+
+Reference interface mirrored: the MoE block of yuhai-china/hy3's GPU backend,
+gpu_ffn_moe (hy3_gpu.cu:706-738) and its upload in hy3_gpu_init
+(hy3_gpu.cu:580-595), with the CPU semantics of forward_layer_moe
+(hy3.c:1266-1325).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+__all__ = ["lib", "lib_path", "MoELayer", "HY3XError", "D_MODEL", "D_FF", "N_EXPERT",
+           "K_MAX", "Q4K_MATRIX_BYTES", "ROUTE_SCALE", "SHARED", "synth_key",
+           "synth_normal", "synth_uniform_sym", "synth_zipf_bias"]
+
+D_MODEL = 4096
+D_FF = 1536
+N_EXPERT = 192
+SHARED = 192
+K_MAX = 8
+Q4K_BLOCK = 144
+Q4K_MATRIX_BYTES = 3538944
+ROUTE_SCALE = 2.826
+# Tensor kinds of the synthetic-input specification.
+T_X, T_NORM, T_ROUTER, T_BIAS, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+lib_path = os.path.join(_HERE, "libhy3x.so")
+_lib = None
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int
+U32 = ctypes.c_uint32
+U64 = ctypes.c_uint64
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+
+_SIGS = {
+    "hy3x_last_error": (ctypes.c_char_p, []),
+    "hy3x_set_device": (I32, [I32]),
+    "hy3x_layer_create": (I32, [ctypes.POINTER(P), I32]),
+    "hy3x_layer_destroy": (I32, [P]),
+    "hy3x_layer_set_router": (I32, [P, P, P, P]),
+    "hy3x_layer_set_expert_q4k": (I32, [P, I32, P, P, P, I32]),
+    "hy3x_layer_expert_ptr": (I32, [P, I32, I32, ctypes.POINTER(P)]),
+    "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
+    "hy3x_layer_last_routing": (I32, [P, P, P, P]),
+    "hy3x_layer_set_path": (I32, [P, I32]),
+    "hy3x_synth_layer_experts": (I32, [P, U64, U32]),
+    "hy3x_synth_quantize_q4k": (I32, [P, P, I64, P]),
+    "hy3x_synth_key": (U64, [U64, U32, U32, U32]),
+    "hy3x_synth_normal": (None, [P, I64, U64, U64, F32, F32]),
+    "hy3x_synth_uniform_sym": (None, [P, I64, U64, F32]),
+    "hy3x_synth_zipf_bias": (None, [P, I32, U64]),
+}
+
+
+class HY3XError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libhy3x.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(lib_path):
+            raise HY3XError(f"{lib_path} is missing: build it with `python -m hy3_amd.build`")
+        h = ctypes.CDLL(lib_path)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise HY3XError(f"hy3x error {rc}: {lib().hy3x_last_error().decode()}")
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        assert a.flags["C_CONTIGUOUS"]
+        return a.ctypes.data
+    if hasattr(a, "data_ptr"):
+        return a.data_ptr()
+    return int(a)
+
+
+def synth_key(seed, layer, kind, index=0):
+    return lib().hy3x_synth_key(seed, layer, kind, index)
+
+
+def synth_normal(n, key, sigma, offset=0.0, first=0):
+    out = np.empty(n, np.float32)
+    lib().hy3x_synth_normal(out.ctypes.data, n, key, first, sigma, offset)
+    return out
+
+
+def synth_uniform_sym(n, key, a):
+    out = np.empty(n, np.float32)
+    lib().hy3x_synth_uniform_sym(out.ctypes.data, n, key, a)
+    return out
+
+
+def synth_zipf_bias(n_expert, seed):
+    out = np.empty(n_expert, np.float32)
+    lib().hy3x_synth_zipf_bias(out.ctypes.data, n_expert, seed)
+    return out
+
+
+class MoELayer:
+    """One Hy3 MoE FFN layer resident on the current HIP device."""
+
+    def __init__(self, max_tokens):
+        h = P()
+        _check(lib().hy3x_layer_create(ctypes.byref(h), max_tokens))
+        self._h = h
+        self.max_tokens = max_tokens
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().hy3x_layer_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_router(self, norm_w, router, bias=None):
+        norm_w = np.ascontiguousarray(norm_w, np.float32)
+        router = np.ascontiguousarray(router, np.float32)
+        assert norm_w.size == D_MODEL and router.size == N_EXPERT * D_MODEL
+        if bias is not None:
+            bias = np.ascontiguousarray(bias, np.float32)
+            assert bias.size == N_EXPERT
+        _check(lib().hy3x_layer_set_router(self._h, _ptr(norm_w), _ptr(router), _ptr(bias)))
+
+    def set_expert_q4k(self, expert, gate, up, down, on_device=False):
+        if not on_device:
+            gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+            assert gate.size == up.size == down.size == Q4K_MATRIX_BYTES
+        _check(lib().hy3x_layer_set_expert_q4k(self._h, expert, _ptr(gate), _ptr(up), _ptr(down),
+                                               1 if on_device else 0))
+
+    def expert_ptr(self, expert, matrix):
+        p = P()
+        _check(lib().hy3x_layer_expert_ptr(self._h, expert, matrix, ctypes.byref(p)))
+        return p.value
+
+    def synth_experts(self, seed, layer_index=0):
+        _check(lib().hy3x_synth_layer_experts(self._h, seed, layer_index))
+
+    def set_path(self, path):
+        _check(lib().hy3x_layer_set_path(self._h, path))
+
+    def forward(self, x_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE, stream=None):
+        """In-place MoE block on device memory x[T x 4096] (fp32)."""
+        _check(lib().hy3x_layer_forward(self._h, x_dev_ptr, T, K, scale, stream))
+
+    def last_routing(self, T, K):
+        ids = np.empty((T, K), np.int32)
+        wpre = np.empty((T, K), np.float32)
+        w = np.empty((T, K), np.float32)
+        _check(lib().hy3x_layer_last_routing(self._h, ids.ctypes.data, wpre.ctypes.data,
+                                             w.ctypes.data))
+        return ids, wpre, w

@@ -1,0 +1,61 @@
+// hy3x_common.h -- shared constants and device helpers for the gfx950 MoE block.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace hy3x {
+
+constexpr int D = 4096;        // hidden size
+constexpr int F = 1536;        // expert intermediate size
+constexpr int E = 192;         // routed experts; expert index E is the shared expert
+constexpr int KMAX = 8;        // top-K upper bound
+constexpr int QK = 256;        // weights per Q4_K super-block
+constexpr int QB = 144;        // bytes per Q4_K super-block
+constexpr int64_t MAT_BYTES = 3538944;          // one 1536x4096 matrix in Q4_K
+constexpr int64_t EXPERT_BYTES = 3 * MAT_BYTES;  // gate | up | down
+constexpr int WAVE = 64;
+
+// fp16 -> fp32 exactly as hy3.c:354-369 decodes Q4_K d/dmin: exponent 0
+// (zero and subnormal halves) becomes 2^-15 * (1 + mant/1024).
+__device__ __forceinline__ float fp16_quirk(uint32_t h) {
+  const uint32_t ex = (h >> 10) & 31u;
+  const uint32_t e32 = ex == 0u ? 112u : (ex == 31u ? 255u : ex + 112u);
+  return __uint_as_float(((h & 0x8000u) << 16) | (e32 << 23) | ((h & 0x3ffu) << 13));
+}
+
+// Activation staging for the Q4_K dot kernels ("pair-staged" fp16 layout).
+// A length-K vector is split into groups of 64 elements (group g = Q4_K block
+// g/4, sub-block pair g%4: elements 0..31 are the low-nibble sub-block,
+// 32..63 the high-nibble one). Each group is 32 dwords of fp16 pairs so that
+// dword j of the weights' qs, unpacked with two masks and one shift, meets its
+// activations in dot2 order:
+//   dword 4j+0 = (x[4j+0],    x[4j+2]   )   low nibbles of bytes 0,2
+//   dword 4j+1 = (x[32+4j+0], x[32+4j+2])   high nibbles of bytes 0,2
+//   dword 4j+2 = (x[4j+1],    x[4j+3]   )   low nibbles of bytes 1,3
+//   dword 4j+3 = (x[32+4j+1], x[32+4j+3])   high nibbles of bytes 1,3
+// Returns the fp16 (half-word) index of element i within the staged vector.
+__host__ __device__ __forceinline__ int stage_index(int i) {
+  const int g = i >> 6, r = i & 63, hi = r >> 5, l = r & 31;
+  const int j = l >> 2, e = l & 3;
+  return g * 64 + 2 * (4 * j + hi + ((e & 1) << 1)) + (e >> 1);
+}
+
+// 64-lane xor-butterfly sum (every lane ends with the total). The addition
+// order is fixed: v_l += v_{l^o} for o = 32, 16, 8, 4, 2, 1.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over each 32-lane half (lanes 0..31 and 32..63 reduced separately).
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+}  // namespace hy3x

@@ -1,0 +1,172 @@
+// hy3x_gemv.hip -- grouped wavefront-reduction GEMV expert kernels (decode)
+// and the weighted combine + residual.
+//
+// Work comes from the device tile list (k_dispatch): a tile is one expert and
+// up to NT of its slots. The weights of a tile are streamed from HBM once,
+// with 16-byte loads (each lane: the block header + 32 bytes of nibbles), and
+// dotted against the NT staged activations held in registers. Replaces
+// moe_matmul_q4k_id_gate_up_kernel / silu_mul_kernel / moe_matmul_q4k_id_kernel
+// / moe_combine_id_kernel / add_kernel (hy3_gpu.cu:96-130, 140-142, 461-463)
+// and the CPU loops hy3.c:1293-1325.
+#include "hy3x_q4k.h"
+
+namespace hy3x {
+
+// Slot -> token: routed slots are t*K + k, shared-expert slots T*K + t.
+__device__ __forceinline__ int slot_token(int slot, int T, int K) {
+  return slot < T * K ? slot / K : slot - T * K;
+}
+
+// gate/up + SwiGLU. Block = 4 waves x 4 rows = 16 rows of the 1536; a wave
+// covers one 4096-wide row (64 groups, one per lane). h = silu(g) * u is
+// written pair-staged (fp16) for the down kernel.
+template <int NT>
+__global__ __launch_bounds__(256) void k_gateup_gemv(const uint8_t *__restrict__ wq,
+                                                     const __half *__restrict__ s16,
+                                                     const int32_t *__restrict__ list,
+                                                     const int4 *__restrict__ tiles,
+                                                     const int32_t *__restrict__ n_tiles, int T,
+                                                     int K, __half *__restrict__ h16) {
+  constexpr int RPWAVE = 4, RPB = 16, CH = F / RPB;
+  const int tile = blockIdx.x / CH, rc = blockIdx.x % CH;
+  if (tile >= *n_tiles) return;
+  const int4 td = tiles[tile];
+  const int e = td.x, o = td.y, n = td.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = lane >> 2, p = lane & 3;
+  const ScaleSel sel(p);
+
+  uint32_t X[NT][32];
+  float slo[NT], shi[NT];
+  int slot[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++) {
+    slot[tt] = 0;
+    slo[tt] = shi[tt] = 0.0f;
+    if (tt < n) {
+      slot[tt] = list[o + tt];
+      load_group_x(s16 + (size_t)slot_token(slot[tt], T, K) * D, lane, X[tt]);
+      group_sums(X[tt], slo[tt], shi[tt]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; j++) X[tt][j] = 0u;
+    }
+  }
+  const uint8_t *gbase = wq + (size_t)e * EXPERT_BYTES + (size_t)b * QB;
+  const uint8_t *ubase = gbase + MAT_BYTES;
+  const int r0 = rc * RPB + wave * RPWAVE;
+#pragma unroll
+  for (int rr = 0; rr < RPWAVE; rr++) {
+    const int r = r0 + rr;
+    const uint8_t *gp = gbase + (size_t)r * (D / QK) * QB;
+    const uint8_t *up = ubase + (size_t)r * (D / QK) * QB;
+    const uint4 gh = *reinterpret_cast<const uint4 *>(gp);
+    const uint4 g0 = *reinterpret_cast<const uint4 *>(gp + 16 + 32 * p);
+    const uint4 g1 = *reinterpret_cast<const uint4 *>(gp + 32 + 32 * p);
+    const uint4 uh = *reinterpret_cast<const uint4 *>(up);
+    const uint4 u0 = *reinterpret_cast<const uint4 *>(up + 16 + 32 * p);
+    const uint4 u1 = *reinterpret_cast<const uint4 *>(up + 32 + 32 * p);
+    const BlockScale gs = block_scale(gh, sel), us = block_scale(uh, sel);
+    uint32_t P[32];
+    float gv[NT], uv[NT];
+    unpack_group(g0, g1, P);
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) gv[tt] = group_dot(P, X[tt], slo[tt], shi[tt], gs);
+    unpack_group(u0, u1, P);
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) uv[tt] = group_dot(P, X[tt], slo[tt], shi[tt], us);
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+      const float g = wave_sum(gv[tt]), u = wave_sum(uv[tt]);
+      if (lane == 0 && tt < n) h16[(size_t)slot[tt] * F + stage_index(r)] = __float2half(silu(g) * u);
+    }
+  }
+}
+
+// down: [4096 x 1536] per expert; a row is 24 groups, so each 32-lane half of
+// a wave takes one row (lanes 24..31 idle). Block = 4 waves x 8 rows = 32 rows.
+// out[slot][row] fp32.
+template <int NT>
+__global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ wq,
+                                                   const __half *__restrict__ h16,
+                                                   const int32_t *__restrict__ list,
+                                                   const int4 *__restrict__ tiles,
+                                                   const int32_t *__restrict__ n_tiles,
+                                                   float *__restrict__ out) {
+  constexpr int RPWAVE = 8, RPB = 32, CH = D / RPB, G = F / 64;
+  const int tile = blockIdx.x / CH, rc = blockIdx.x % CH;
+  if (tile >= *n_tiles) return;
+  const int4 td = tiles[tile];
+  const int e = td.x, o = td.y, n = td.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hw = lane >> 5, gl = lane & 31;
+  const bool active = gl < G;
+  const int b = gl >> 2, p = gl & 3;
+  const ScaleSel sel(p);
+
+  uint32_t X[NT][32];
+  float slo[NT], shi[NT];
+  int slot[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++) {
+    slot[tt] = 0;
+    slo[tt] = shi[tt] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) X[tt][j] = 0u;
+    if (tt < n) {
+      slot[tt] = list[o + tt];
+      if (active) {
+        load_group_x(h16 + (size_t)slot[tt] * F, gl, X[tt]);
+        group_sums(X[tt], slo[tt], shi[tt]);
+      }
+    }
+  }
+  const uint8_t *dbase = wq + (size_t)e * EXPERT_BYTES + 2 * MAT_BYTES + (size_t)b * QB;
+  const int r0 = rc * RPB + wave * RPWAVE;
+#pragma unroll
+  for (int it = 0; it < RPWAVE / 2; it++) {
+    const int r = r0 + 2 * it + hw;
+    float dv[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) dv[tt] = 0.0f;
+    if (active) {
+      const uint8_t *dp = dbase + (size_t)r * (F / QK) * QB;
+      const uint4 hd = *reinterpret_cast<const uint4 *>(dp);
+      const uint4 q0 = *reinterpret_cast<const uint4 *>(dp + 16 + 32 * p);
+      const uint4 q1 = *reinterpret_cast<const uint4 *>(dp + 32 + 32 * p);
+      const BlockScale bs = block_scale(hd, sel);
+      uint32_t P[32];
+      unpack_group(q0, q1, P);
+#pragma unroll
+      for (int tt = 0; tt < NT; tt++) dv[tt] = group_dot(P, X[tt], slo[tt], shi[tt], bs);
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+      const float v = half_sum(dv[tt]);
+      if (gl == 0 && tt < n) out[(size_t)slot[tt] * D + r] = v;
+    }
+  }
+}
+
+// y = x + (shared + sum_k w_k * routed_k), k in selection order (hy3.c:1302,
+// 1318-1319, 1324-1325).
+__global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
+                                                 const float *__restrict__ out,
+                                                 const float *__restrict__ w, int T, int K) {
+  const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+  float eo = 0.0f;
+  for (int k = 0; k < K; k++) eo = __builtin_fmaf(w[t * K + k], out[(size_t)(t * K + k) * D + i], eo);
+  const float sh = out[(size_t)(T * K + t) * D + i];
+  x[(size_t)t * D + i] = x[(size_t)t * D + i] + (sh + eo);
+}
+
+template __global__ void k_gateup_gemv<1>(const uint8_t *, const __half *, const int32_t *,
+                                          const int4 *, const int32_t *, int, int, __half *);
+template __global__ void k_gateup_gemv<4>(const uint8_t *, const __half *, const int32_t *,
+                                          const int4 *, const int32_t *, int, int, __half *);
+template __global__ void k_down_gemv<1>(const uint8_t *, const __half *, const int32_t *,
+                                        const int4 *, const int32_t *, float *);
+template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, const int32_t *,
+                                        const int4 *, const int32_t *, float *);
+
+}  // namespace hy3x

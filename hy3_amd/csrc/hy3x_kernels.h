@@ -1,0 +1,36 @@
+// hy3x_kernels.h -- kernel declarations shared by the translation units.
+#pragma once
+#include "hy3x_common.h"
+
+namespace hy3x {
+
+__global__ void k_router_gemv(const float *x, const float *norm_w, const float *router,
+                              const float *bias, int has_bias, int K, float scale, float *logits,
+                              __half *s16, int32_t *ids, float *wpre, float *wout,
+                              unsigned *tickets);
+__global__ void k_dispatch(const int32_t *ids, int T, int K, int NT, int32_t *list, int4 *tiles,
+                           int32_t *n_tiles, int max_tiles, int32_t *counts_out);
+template <int NT>
+__global__ void k_gateup_gemv(const uint8_t *wq, const __half *s16, const int32_t *list,
+                              const int4 *tiles, const int32_t *n_tiles, int T, int K,
+                              __half *h16);
+template <int NT>
+__global__ void k_down_gemv(const uint8_t *wq, const __half *h16, const int32_t *list,
+                            const int4 *tiles, const int32_t *n_tiles, float *out);
+__global__ void k_combine(float *x, const float *out, const float *w, int T, int K);
+
+extern template __global__ void k_gateup_gemv<1>(const uint8_t *, const __half *, const int32_t *,
+                                                 const int4 *, const int32_t *, int, int,
+                                                 __half *);
+extern template __global__ void k_gateup_gemv<4>(const uint8_t *, const __half *, const int32_t *,
+                                                 const int4 *, const int32_t *, int, int,
+                                                 __half *);
+extern template __global__ void k_down_gemv<1>(const uint8_t *, const __half *, const int32_t *,
+                                               const int4 *, const int32_t *, float *);
+extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, const int32_t *,
+                                               const int4 *, const int32_t *, float *);
+
+__global__ void k_synth_q4k(uint8_t *dst, int64_t nblocks, uint64_t seed, uint32_t layer,
+                            const float *src);
+
+}  // namespace hy3x

@@ -1,0 +1,231 @@
+// hy3x_layer.hip -- the layer object and the C ABI (include/hy3x_moe.h).
+//
+// Device memory of a layer:
+//   wq       193 experts x [gate | up | down] Q4_K, 10,616,832 B per expert, in
+//            the unchanged GGUF block layout (row r of a matrix = blocks
+//            [r*C/256, (r+1)*C/256)); expert 192 is the shared expert;
+//   norm_w, router, bias   fp32 as in GGUF;
+//   scratch  per token: staged s (8 KB), logits, routing; per slot (T*(K+1)):
+//            staged h (3 KB) and the expert output row (16 KB).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+#include "../../include/hy3x_moe.h"
+#include "hy3x_kernels.h"
+
+using namespace hy3x;
+
+struct hy3x_layer {
+  int device = 0;
+  int max_tokens = 0;
+  uint8_t *wq = nullptr;
+  float *norm_w = nullptr, *router = nullptr, *bias = nullptr;
+  int has_bias = 0, router_set = 0;
+  float *logits = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
+  __half *s16 = nullptr, *h16 = nullptr;
+  int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
+  int4 *tiles = nullptr;
+  unsigned *tickets = nullptr;
+  int max_tiles_alloc = 0;
+  int last_T = 0, last_K = 0;
+  hipStream_t last_stream = nullptr;
+  int path = 0;
+};
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(call)                                                                  \
+  do {                                                                                 \
+    hipError_t e_ = (call);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return fail(HY3X_E_HIP, "%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                  __FILE__, __LINE__);                                                 \
+  } while (0)
+
+template <class P>
+static int dalloc(P **p, size_t bytes) {
+  if (hipMalloc((void **)p, bytes) != hipSuccess) {
+    *p = nullptr;
+    (void)hipGetLastError();
+    return fail(HY3X_E_NOMEM, "hipMalloc(%zu) failed", bytes);
+  }
+  return HY3X_OK;
+}
+
+static int max_tiles_for(int T, int K, int NT) {
+  const int n = T * K;
+  return n / NT + std::min(E, n) + (T + NT - 1) / NT + 1;
+}
+
+extern "C" {
+
+const char *hy3x_last_error(void) { return g_err.c_str(); }
+
+int hy3x_set_device(int device) {
+  HIP_TRY(hipSetDevice(device));
+  return HY3X_OK;
+}
+
+int hy3x_layer_destroy(hy3x_layer *L) {
+  if (!L) return HY3X_OK;
+  void *ptrs[] = {L->wq,   L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
+                  L->w,    L->out,    L->s16,    L->h16,     L->ids,     L->list,
+                  L->n_tiles, L->counts, L->tiles, L->tickets};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  delete L;
+  return HY3X_OK;
+}
+
+int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
+  if (!out) return fail(HY3X_E_ARG, "out is NULL");
+  *out = nullptr;
+  if (max_tokens < 1 || max_tokens > (1 << 16))
+    return fail(HY3X_E_ARG, "max_tokens %d out of range [1, 65536]", max_tokens);
+  hy3x_layer *L = new hy3x_layer();
+  HIP_TRY(hipGetDevice(&L->device));
+  L->max_tokens = max_tokens;
+  const size_t T = (size_t)max_tokens, slots = T * (KMAX + 1);
+  L->max_tiles_alloc = max_tiles_for(max_tokens, KMAX, 1);
+  int rc = HY3X_OK;
+  if ((rc = dalloc(&L->wq, (size_t)(E + 1) * EXPERT_BYTES)) ||
+      (rc = dalloc(&L->norm_w, D * sizeof(float))) ||
+      (rc = dalloc(&L->router, (size_t)E * D * sizeof(float))) ||
+      (rc = dalloc(&L->bias, E * sizeof(float))) ||
+      (rc = dalloc(&L->logits, T * E * sizeof(float))) ||
+      (rc = dalloc(&L->wpre, T * KMAX * sizeof(float))) ||
+      (rc = dalloc(&L->w, T * KMAX * sizeof(float))) ||
+      (rc = dalloc(&L->ids, T * KMAX * sizeof(int32_t))) ||
+      (rc = dalloc(&L->s16, T * D * sizeof(__half))) ||
+      (rc = dalloc(&L->h16, slots * F * sizeof(__half))) ||
+      (rc = dalloc(&L->out, slots * D * sizeof(float))) ||
+      (rc = dalloc(&L->list, slots * sizeof(int32_t))) ||
+      (rc = dalloc(&L->tiles, (size_t)L->max_tiles_alloc * sizeof(int4))) ||
+      (rc = dalloc(&L->n_tiles, sizeof(int32_t))) ||
+      (rc = dalloc(&L->counts, (E + 1) * sizeof(int32_t))) ||
+      (rc = dalloc(&L->tickets, T * sizeof(unsigned)))) {
+    hy3x_layer_destroy(L);
+    return rc;
+  }
+  if (hipMemset(L->tickets, 0, T * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess) {
+    hy3x_layer_destroy(L);
+    return fail(HY3X_E_HIP, "hipMemset failed");
+  }
+  *out = L;
+  return HY3X_OK;
+}
+
+int hy3x_layer_set_router(hy3x_layer *L, const float *norm_w, const float *router,
+                          const float *expert_bias) {
+  if (!L || !norm_w || !router) return fail(HY3X_E_ARG, "NULL argument");
+  HIP_TRY(hipMemcpy(L->norm_w, norm_w, D * sizeof(float), hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(L->router, router, (size_t)E * D * sizeof(float), hipMemcpyHostToDevice));
+  if (expert_bias) HIP_TRY(hipMemcpy(L->bias, expert_bias, E * sizeof(float), hipMemcpyHostToDevice));
+  L->has_bias = expert_bias != nullptr;
+  L->router_set = 1;
+  return HY3X_OK;
+}
+
+int hy3x_layer_expert_ptr(hy3x_layer *L, int expert, int matrix, void **ptr) {
+  if (!L || !ptr) return fail(HY3X_E_ARG, "NULL argument");
+  if (expert < 0 || expert > E || matrix < 0 || matrix > 2)
+    return fail(HY3X_E_ARG, "expert %d / matrix %d out of range", expert, matrix);
+  *ptr = L->wq + (size_t)expert * EXPERT_BYTES + (size_t)matrix * MAT_BYTES;
+  return HY3X_OK;
+}
+
+int hy3x_layer_set_expert_q4k(hy3x_layer *L, int expert, const void *gate, const void *up,
+                              const void *down, int src_on_device) {
+  if (!L || !gate || !up || !down) return fail(HY3X_E_ARG, "NULL argument");
+  if (expert < 0 || expert > E) return fail(HY3X_E_ARG, "expert %d out of range [0,192]", expert);
+  const hipMemcpyKind kind = src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  uint8_t *dst = L->wq + (size_t)expert * EXPERT_BYTES;
+  HIP_TRY(hipMemcpy(dst, gate, MAT_BYTES, kind));
+  HIP_TRY(hipMemcpy(dst + MAT_BYTES, up, MAT_BYTES, kind));
+  HIP_TRY(hipMemcpy(dst + 2 * MAT_BYTES, down, MAT_BYTES, kind));
+  return HY3X_OK;
+}
+
+int hy3x_layer_set_path(hy3x_layer *L, int path) {
+  if (!L || path < 0 || path > 2) return fail(HY3X_E_ARG, "bad path");
+  L->path = path;
+  return HY3X_OK;
+}
+
+int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
+  if (!L || !x) return fail(HY3X_E_ARG, "NULL argument");
+  if (T < 1 || T > L->max_tokens) return fail(HY3X_E_ARG, "T=%d outside [1,%d]", T, L->max_tokens);
+  if (K < 1 || K > KMAX) return fail(HY3X_E_ARG, "K=%d outside [1,8]", K);
+  if (!L->router_set) return fail(HY3X_E_STATE, "router not set");
+  hipStream_t st = (hipStream_t)stream;
+  k_router_gemv<<<dim3(E / 4, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias, L->has_bias, K,
+                                                 scale, L->logits, L->s16, L->ids, L->wpre, L->w,
+                                                 L->tickets);
+  const int NT = T == 1 ? 1 : 4;
+  const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
+  k_dispatch<<<1, 1024, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts);
+  if (NT == 1) {
+    k_gateup_gemv<1><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
+                                                    T, K, L->h16);
+    k_down_gemv<1><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
+                                                  L->out);
+  } else {
+    k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
+                                                    T, K, L->h16);
+    k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
+                                                  L->out);
+  }
+  k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+  HIP_TRY(hipGetLastError());
+  L->last_T = T;
+  L->last_K = K;
+  L->last_stream = st;
+  return HY3X_OK;
+}
+
+int hy3x_layer_last_routing(hy3x_layer *L, int32_t *ids, float *wpre, float *w) {
+  if (!L) return fail(HY3X_E_ARG, "NULL layer");
+  if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
+  HIP_TRY(hipStreamSynchronize(L->last_stream));
+  const size_t n = (size_t)L->last_T * L->last_K;
+  if (ids) HIP_TRY(hipMemcpy(ids, L->ids, n * sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (wpre) HIP_TRY(hipMemcpy(wpre, L->wpre, n * sizeof(float), hipMemcpyDeviceToHost));
+  if (w) HIP_TRY(hipMemcpy(w, L->w, n * sizeof(float), hipMemcpyDeviceToHost));
+  return HY3X_OK;
+}
+
+int hy3x_synth_layer_experts(hy3x_layer *L, uint64_t seed, uint32_t layer_index) {
+  if (!L) return fail(HY3X_E_ARG, "NULL layer");
+  const int64_t nblocks = (int64_t)(E + 1) * EXPERT_BYTES / QB;
+  k_synth_q4k<<<(unsigned)((nblocks + 3) / 4), 256>>>(L->wq, nblocks, seed, layer_index, nullptr);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipDeviceSynchronize());
+  return HY3X_OK;
+}
+
+int hy3x_synth_quantize_q4k(const float *src, void *dst, int64_t n, void *stream) {
+  if (!src || !dst || n <= 0 || n % QK) return fail(HY3X_E_ARG, "bad quantize arguments");
+  const int64_t nblocks = n / QK;
+  k_synth_q4k<<<(unsigned)((nblocks + 3) / 4), 256, 0, (hipStream_t)stream>>>(
+      (uint8_t *)dst, nblocks, 0, 0, src);
+  HIP_TRY(hipGetLastError());
+  return HY3X_OK;
+}
+
+}  // extern "C"

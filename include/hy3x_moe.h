@@ -1,0 +1,122 @@
+/*
+ * hy3x_moe.h -- C ABI of the MI355X (gfx950) Hy3 MoE FFN block.
+ *
+ * One library, libhy3x.so, built by hipcc for gfx950. Plain C types only.
+ * Every call returns 0 on success or a negative HY3X_E* code; the message of
+ * the last failure on the calling thread is available from hy3x_last_error().
+ * Nothing in this library calls exit() (the reference aborts the process on
+ * any CUDA error, hy3_gpu.cu:17-20).
+ *
+ * Reference interface replaced (yuhai-china/hy3):
+ *  - gpu_ffn_moe()          hy3_gpu.cu:706-738  -> hy3x_layer_forward()
+ *    (router GEMV + router_topk_kernel + routed gate_up/silu/down kernels +
+ *    shared-expert GEMMs + moe_combine_id_kernel, one token per call), and
+ *    the per-token prefill loop around it, hy3_gpu.cu:836-837, which the
+ *    batched forward (T tokens per call) replaces;
+ *  - the MoE part of hy3_gpu_init(), hy3_gpu.cu:580-595 (router/bias upload,
+ *    Q4_K expert upload through upload_q4k_compressed hy3_gpu.cu:515, device
+ *    pointer tables) -> hy3x_layer_create / hy3x_layer_set_router /
+ *    hy3x_layer_set_expert_q4k;
+ *  - the MoE scratch of hy3_gpu_init(), hy3_gpu.cu:616-621 -> owned by the
+ *    layer object, sized by max_tokens;
+ *  - the CPU MoE block forward_layer_moe(), hy3.c:1266-1325, whose semantics
+ *    (RMSNorm, sigmoid + expert_bias top-K, renormalised weights x2.826,
+ *    shared expert, combine, residual) this forward computes.
+ */
+#ifndef HY3X_MOE_H
+#define HY3X_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HY3X_OK 0
+#define HY3X_E_ARG (-1)     /* bad argument (NULL, range, size)            */
+#define HY3X_E_HIP (-2)     /* HIP runtime error                           */
+#define HY3X_E_NOMEM (-3)   /* device allocation failed                    */
+#define HY3X_E_STATE (-4)   /* call out of order (e.g. weights not set)    */
+
+#define HY3X_D_MODEL 4096   /* HY3_N_EMBD       hy3.h:33 */
+#define HY3X_D_FF 1536      /* HY3_MOE_INTERMED hy3.h:42 */
+#define HY3X_N_EXPERT 192   /* HY3_N_EXPERT     hy3.h:39 */
+#define HY3X_K_MAX 8        /* HY3_N_EXPERT_USED hy3.h:40 */
+#define HY3X_Q4K_BLOCK 144  /* sizeof(block_q4_K) hy3.c:405-410 */
+/* Q4_K bytes of one [1536 x 4096] or [4096 x 1536] matrix. */
+#define HY3X_Q4K_MATRIX_BYTES 3538944
+#define HY3X_ROUTE_SCALE 2.826f /* hy3.c:1289, hy3_gpu.cu:717 */
+
+typedef struct hy3x_layer hy3x_layer;
+
+/* Message for the last failed call on this thread ("" if none). */
+const char *hy3x_last_error(void);
+
+/* Select the HIP device for subsequent calls on this thread. */
+int hy3x_set_device(int device);
+
+/* Create one MoE layer on the current device, with scratch for up to
+ * max_tokens tokens per forward. Replaces the MoE allocations of
+ * hy3_gpu_init (hy3_gpu.cu:580-595, 616-621). Device memory: 193 experts x
+ * 3 matrices of Q4_K (2.05 GB) + router (3 MB) + scratch (~36 KB/token). */
+int hy3x_layer_create(hy3x_layer **out, int max_tokens);
+int hy3x_layer_destroy(hy3x_layer *layer);
+
+/* Router-side tensors, host pointers, copied to the device:
+ * norm_w[4096] (ffn_norm, F32), router[192 x 4096] (ffn_gate_inp, F32,
+ * row-major as in GGUF), expert_bias[192] or NULL when the layer has no bias
+ * (has_expert_bias == false, hy3.c:781-787). Mirrors hy3_gpu.cu:580,589. */
+int hy3x_layer_set_router(hy3x_layer *layer, const float *norm_w, const float *router,
+                          const float *expert_bias);
+
+/* Q4_K expert matrices in the unchanged GGUF block layout (the bytes
+ * hy3_weight.data points at for ffn_{gate,up,down}_exps[e], hy3.h:137-139):
+ * gate/up [1536 x 4096], down [4096 x 1536], HY3X_Q4K_MATRIX_BYTES each.
+ * expert in [0,192) is a routed expert; expert == 192 is the shared expert
+ * (ffn_{gate,up,down}_shexp) in Q4_K. src_on_device != 0: the pointers are
+ * device pointers. Replaces upload_q4k_compressed (hy3_gpu.cu:515,590). */
+int hy3x_layer_set_expert_q4k(hy3x_layer *layer, int expert, const void *gate, const void *up,
+                              const void *down, int src_on_device);
+
+/* Device address of expert e's matrix m (0 gate, 1 up, 2 down) inside the
+ * layer's weight arena, for callers that fill the arena directly. */
+int hy3x_layer_expert_ptr(hy3x_layer *layer, int expert, int matrix, void **ptr);
+
+/* The MoE block for T tokens, in place on device memory:
+ *   s = rmsnorm(x) * norm_w;  route (sigmoid + bias, top-K, renorm, x scale);
+ *   x += shared(s) + sum_k w_k * expert_k(s)
+ * x: device pointer to [T x 4096] fp32. 1 <= T <= max_tokens, 1 <= K <= 8.
+ * stream: a hipStream_t (NULL = default stream). Asynchronous: returns after
+ * enqueueing. Calls on one layer must not overlap (shared scratch), as with
+ * the reference's ctx singleton buffers (hy3_gpu.cu:483, 616-621). */
+int hy3x_layer_forward(hy3x_layer *layer, float *x, int T, int K, float scale, void *stream);
+
+/* Routing of the last forward, copied to host buffers (synchronises on the
+ * stream): ids[T x K] int32 in selection order, wpre[T x K] = sigma / sum
+ * (before the scale), w[T x K] (after). Any pointer may be NULL. */
+int hy3x_layer_last_routing(hy3x_layer *layer, int32_t *ids, float *wpre, float *w);
+
+/* Execution-path override for tests: 0 = automatic (by T), 1 = force the
+ * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path. */
+int hy3x_layer_set_path(hy3x_layer *layer, int path);
+
+/* ---- synthetic inputs (test / benchmark data, not part of the MoE path) ----
+ * Device-side generator + Q4_K quantiser for the seeded synthetic layers the
+ * benchmark configurations describe. The quantiser reproduces hy3_convert.c's
+ * quantize_row_q4_K (hy3_convert.c:605-651) as built by its Makefile. */
+/* Fill every expert (0..192) of the layer from (seed, layer_index). */
+int hy3x_synth_layer_experts(hy3x_layer *layer, uint64_t seed, uint32_t layer_index);
+/* Quantise n fp32 values (device pointers; n multiple of 256) to Q4_K. */
+int hy3x_synth_quantize_q4k(const float *src, void *dst, int64_t n, void *stream);
+/* Host-side generators for the small tensors (bit-identical to the spec). */
+uint64_t hy3x_synth_key(uint64_t seed, uint32_t layer, uint32_t kind, uint32_t index);
+void hy3x_synth_normal(float *dst, int64_t n, uint64_t key, uint64_t first, float sigma,
+                       float offset);
+void hy3x_synth_uniform_sym(float *dst, int64_t n, uint64_t key, float a);
+void hy3x_synth_zipf_bias(float *dst, int n_expert, uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,87 @@
+/*
+ * ref_shim_hy3.c -- drives the reference CPU MoE block (TEST INFRASTRUCTURE).
+ *
+ * Compiles yuhai-china/hy3's own hy3.c from /root/reference (never copied)
+ * with its Makefile flags and exports:
+ *  - hy3ref_fp16_to_fp32, hy3ref_dequant_q4k, hy3ref_topk_select,
+ *    hy3ref_mul_mat: thin wrappers over the static helpers
+ *    (hy3.c:354-369, 1019-1043, 654-666, 1073-1155);
+ *  - hy3ref_moe_forward: runs the reference's forward_layer_moe (hy3.c:1219)
+ *    once per token on a one-layer in-memory hy3_model whose attention half
+ *    contributes exactly +0 (its q/k/v/o projections carry an unsupported
+ *    ggml type, for which mul_mat_f32 writes zeros, hy3.c:1149-1152). The MoE
+ *    half (hy3.c:1266-1325) is the reference's code, unmodified. After each
+ *    token the router scores sigmoid+bias (scratch2[0..191], written at
+ *    hy3.c:1272-1277 and not overwritten later) are copied out.
+ */
+#include "hy3.c"
+
+#include <limits.h>
+
+float hy3ref_fp16_to_fp32(uint16_t h) { return fp16_to_fp32(h); }
+void hy3ref_dequant_q4k(float *dst, const uint8_t *src, int n) { dequantize_row_q4_K(dst, src, n); }
+void hy3ref_topk_select(float *vals, int *inds, const float *scores, int n, int k) {
+  topk_select(vals, inds, scores, n, k);
+}
+void hy3ref_mul_mat(float *dst, const uint8_t *w, uint32_t type, const float *x, int m, int n) {
+  mul_mat_f32(dst, w, type, x, m, n);
+}
+void hy3ref_set_threads(int n) { omp_set_num_threads(n); }
+
+static hy3_tensor_info ti_f32 = {0}, ti_q4k = {0}, ti_none = {0};
+
+/* x: [T x 4096] updated in place. gate/up/down: 193 host pointers each (index
+ * 192 = shared expert). scores_out: [T x 192] or NULL. quiet: silence the
+ * attention half's "unsupported ggml_type" diagnostics. Returns 0. */
+int hy3ref_moe_forward(float *x, int T, int K, const float *norm_w, const float *router,
+                       const float *bias, int has_bias, const uint8_t *const *gate,
+                       const uint8_t *const *up, const uint8_t *const *down,
+                       float *scores_out, int quiet) {
+  ti_f32.ggml_type = 0;
+  ti_q4k.ggml_type = 12;
+  ti_none.ggml_type = 0x7fffffff;
+  hy3_model *m = (hy3_model *)calloc(1, sizeof(hy3_model));
+  static float ones[HY3_N_EMBD];
+  for (int i = 0; i < HY3_N_EMBD; i++) ones[i] = 1.0f;
+  m->n_expert_used = K;
+  m->scratch = (float *)calloc(1 << 16, sizeof(float));
+  m->scratch2 = (float *)calloc(1 << 16, sizeof(float));
+  m->cache_k = (float *)calloc((size_t)4 * HY3_N_KV_HEAD * HY3_HEAD_DIM, sizeof(float));
+  m->cache_v = (float *)calloc((size_t)4 * HY3_N_KV_HEAD * HY3_HEAD_DIM, sizeof(float));
+  m->rope_attn_factor = 1.0f;
+  m->rope_pos_stride = 1;
+  m->rope_pos_jump_at = INT_MAX;
+  hy3_layer_weights *l = &m->w.layers[1];
+  l->attn_norm.t = &ti_f32; l->attn_norm.data = (const uint8_t *)ones;
+  l->attn_q.t = &ti_none; l->attn_k.t = &ti_none; l->attn_v.t = &ti_none;
+  l->attn_output.t = &ti_none;
+  l->ffn_norm.t = &ti_f32; l->ffn_norm.data = (const uint8_t *)norm_w;
+  l->ffn_gate_inp.t = &ti_f32; l->ffn_gate_inp.data = (const uint8_t *)router;
+  for (int e = 0; e < HY3_N_EXPERT; e++) {
+    l->ffn_gate_exps[e].t = &ti_q4k; l->ffn_gate_exps[e].data = gate[e];
+    l->ffn_up_exps[e].t = &ti_q4k; l->ffn_up_exps[e].data = up[e];
+    l->ffn_down_exps[e].t = &ti_q4k; l->ffn_down_exps[e].data = down[e];
+    l->expert_bias[e] = has_bias ? bias[e] : 0.0f;
+  }
+  l->has_expert_bias = has_bias ? true : false;
+  l->ffn_gate_shexp.t = &ti_q4k; l->ffn_gate_shexp.data = gate[HY3_N_EXPERT];
+  l->ffn_up_shexp.t = &ti_q4k; l->ffn_up_shexp.data = up[HY3_N_EXPERT];
+  l->ffn_down_shexp.t = &ti_q4k; l->ffn_down_shexp.data = down[HY3_N_EXPERT];
+
+  int saved = -1;
+  if (quiet) {
+    fflush(stderr);
+    saved = dup(2);
+    int devnull = open("/dev/null", O_WRONLY);
+    if (devnull >= 0) { dup2(devnull, 2); close(devnull); }
+  }
+  for (int t = 0; t < T; t++) {
+    m->embed = x + (size_t)t * HY3_N_EMBD;
+    m->cache_len = 0;
+    forward_layer_moe(m, 1, 0);
+    if (scores_out) memcpy(scores_out + (size_t)t * HY3_N_EXPERT, m->scratch2, HY3_N_EXPERT * sizeof(float));
+  }
+  if (quiet && saved >= 0) { fflush(stderr); dup2(saved, 2); close(saved); }
+  free(m->scratch); free(m->scratch2); free(m->cache_k); free(m->cache_v); free(m);
+  return 0;
+}
