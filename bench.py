@@ -1,0 +1,211 @@
+"""Benchmark: one Hy3 MoE FFN layer on one MI355X through libhy3x.so.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0..4]
+                    [--secondary] [--cpu-seconds S]
+
+A step is one forward of the MoE block (RMSNorm, router, top-8, 8 routed + 1
+shared Q4_K SwiGLU experts, combine, residual) over one batch of synthetic
+input already resident in HBM. The default workload is config 0 (decode, one
+token), the configuration of the north-star target; --secondary adds one line
+of results per other configuration inside the same JSON object.
+
+Prints ONE JSON line (rank 0). Fields beyond the driver's contract:
+  roofline      dominant kernel stage: algorithmic bytes per launch / its mean
+                duration from HIP events recorded on the launch stream
+  cpu_baseline  the reference CPU MoE block (hy3.c forward_layer_moe built
+                from the reference sources, oracle/_ref) or, when that library
+                is absent, the oracle port, on a bounded token sample
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0
+MAT = 3538944
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=0, help="timed steps (0: per-config default)")
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", type=int, default=0)
+    p.add_argument("--secondary", action="store_true", help="also measure the other configs")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def default_steps(T, n_layers):
+    if n_layers > 1:
+        return 20
+    return {1: 2000, 32: 500}.get(T, 50 if T <= 512 else 10)
+
+
+def stage_bytes(stage, U, T, K):
+    """Algorithmic HBM bytes of one launch of a kernel stage."""
+    if stage == "gateup":
+        return U * 2 * MAT + T * 4096 * 2 + T * (K + 1) * 1536 * 2
+    if stage == "down":
+        return U * MAT + T * (K + 1) * (1536 * 2 + 4096 * 4)
+    if stage == "router":
+        return 192 * 4096 * 4 + 4096 * 4 + T * 4096 * 4 + T * 4096 * 6
+    return 0
+
+
+def measure(torch, H, C, cfg, steps, warmup):
+    layers = []
+    for li in range(cfg.n_layers):
+        L = H.MoELayer(cfg.T)
+        L.synth_experts(cfg.weight_seed, li)
+        nw, rt, b = C.config_tensors(cfg, li)
+        L.set_router(nw, rt, b)
+        layers.append(L)
+    x = torch.from_numpy(C.inputs(cfg.input_seed, cfg.T).copy()).cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        for L in layers:
+            L.forward(x.data_ptr(), cfg.T, cfg.K, stream=stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    for L in layers:
+        L.stats(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    fw, touched = zip(*[L.stats(reset=True) for L in layers])
+    U = sum(touched) / max(sum(fw), 1)  # mean experts touched per layer-forward
+    ms = elapsed * 1e3 / steps
+    tokens_per_s = cfg.T * steps / elapsed
+
+    # per-stage timing pass (HIP events on the launch stream)
+    for L in layers:
+        L.set_timing(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    stages = {}
+    nfw = 0
+    for L in layers:
+        st, n = L.stage_times()
+        nfw += n
+        for k, v in st.items():
+            stages[k] = stages.get(k, 0.0) + v
+        L.set_timing(False)
+    stage_us = {k: v * 1e3 / max(nfw, 1) for k, v in stages.items()}
+    dom = max(("gateup", "down"), key=lambda k: stage_us[k])
+    dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K)
+    achieved = dom_bytes / (stage_us[dom] * 1e-6) / 1e9
+    alg_bytes = C.algorithmic_bytes(cfg.T, U) * cfg.n_layers
+    flops = C.algorithmic_flops(cfg.T, cfg.K) * cfg.n_layers
+    for L in layers:
+        L.close()
+    return dict(
+        tokens_per_s=tokens_per_s, ms_per_step=ms, U=U, layer_GBps=alg_bytes / (ms * 1e-3) / 1e9,
+        layer_TFLOPs=flops / (ms * 1e-3) / 1e12, stage_us=stage_us,
+        roofline=dict(bound="hbm", kernel=dom, achieved=round(achieved, 1), peak=PEAK_HBM_GBS,
+                      unit="GB/s", frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
+                      bytes_per_launch=int(dom_bytes), launch_us=round(stage_us[dom], 3)),
+    )
+
+
+def cpu_baseline(torch, H, C, cfg, seconds):
+    """hy3.c's CPU MoE block on a bounded token sample (same Q4_K bytes)."""
+    from oracle import hy3_oracle as O
+    from hy3_amd import hipmem
+    L = H.MoELayer(1)
+    L.synth_experts(cfg.weight_seed, 0)
+    lay = O.SynthLayer(cfg.weight_seed, 0,
+                       zipf_seed=cfg.input_seed if cfg.zipf_bias else None)
+    for e in range(193):
+        lay.experts[e] = tuple(hipmem.to_host(L.expert_ptr(e, m), MAT) for m in range(3))
+    L.close()
+    ref = O.ref_lib()
+    kind = "reference" if ref is not None else "port"
+    cores = os.cpu_count() or 1
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    if ref is not None:
+        ref.hy3ref_set_threads(cores)
+    else:
+        O.lib().hy3o_set_num_threads(cores)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        x = C.inputs(cfg.input_seed, 1, first_token=n)
+        if ref is not None:
+            lay.ref_forward(x, cfg.K)
+        else:
+            lay.forward(x, cfg.K)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 100000:
+            break
+    return dict(value=round(n / el, 3), unit="tokens/s", cores=cores, kind=kind,
+                sample=f"{n} tokens of config {cfg.index}, one at a time as hy3.c runs its MoE "
+                       f"(forward_layer_moe per token), {el:.1f} s")
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md, not implemented.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import hy3_amd as H
+    from hy3_amd import configs as C
+    torch.cuda.init()
+    cfg = C.CONFIGS[a.config]
+    steps = a.steps or default_steps(cfg.T, cfg.n_layers)
+    r = measure(torch, H, C, cfg, steps, a.warmup)
+    out = {
+        "metric": "MoE-layer tokens/s (decode B=1) and achieved HBM GB/s vs peak",
+        "value": round(r["tokens_per_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": a.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4k-weights/fp16-act/fp32-acc",
+        "data": "synthetic (seeded, BASELINE configs; random-init Q4_K weights)",
+        "config": {"workload": f"config{cfg.index}:{cfg.name}", "tokens": cfg.T,
+                   "layers": cfg.n_layers, "top_k": cfg.K, "experts": "192+1 shared",
+                   "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu"},
+        "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),
+                  "hbm_frac": round(r["layer_GBps"] / PEAK_HBM_GBS, 4),
+                  "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},
+        "roofline": r["roofline"],
+    }
+    if a.secondary:
+        sec = {}
+        for c in C.CONFIGS:
+            if c.index == cfg.index:
+                continue
+            rr = measure(torch, H, C, c, default_steps(c.T, c.n_layers), 3)
+            sec[f"config{c.index}:{c.name}"] = {
+                "tokens_per_s": round(rr["tokens_per_s"], 1),
+                "ms_per_step": round(rr["ms_per_step"], 4),
+                "GB_per_s": round(rr["layer_GBps"], 1), "TFLOP_per_s": round(rr["layer_TFLOPs"], 2),
+                "experts_touched": round(rr["U"], 1),
+                "stage_us": {k: round(v, 1) for k, v in rr["stage_us"].items()},
+                "roofline": rr["roofline"]}
+            torch.cuda.empty_cache()
+        out["secondary"] = sec
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(torch, H, C, cfg, a.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -53,6 +53,9 @@ _SIGS = {
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
+    "hy3x_layer_set_timing": (I32, [P, I32]),
+    "hy3x_layer_stats": (I32, [P, ctypes.POINTER(U64), ctypes.POINTER(U64), I32]),
+    "hy3x_layer_stage_times": (I32, [P, P, I32, ctypes.POINTER(I32)]),
     "hy3x_synth_layer_experts": (I32, [P, U64, U32]),
     "hy3x_synth_quantize_q4k": (I32, [P, P, I64, P]),
     "hy3x_synth_key": (U64, [U64, U32, U32, U32]),
@@ -165,6 +168,24 @@ class MoELayer:
 
     def set_path(self, path):
         _check(lib().hy3x_layer_set_path(self._h, path))
+
+    STAGES = ("router", "dispatch", "gateup", "down", "combine")
+
+    def set_timing(self, enable):
+        _check(lib().hy3x_layer_set_timing(self._h, 1 if enable else 0))
+
+    def stage_times(self):
+        """Accumulated ms per stage since the last reset, and the forward count."""
+        ms = np.zeros(8, np.float32)
+        n = I32()
+        _check(lib().hy3x_layer_stage_times(self._h, ms.ctypes.data, 8, ctypes.byref(n)))
+        return {k: float(ms[i]) for i, k in enumerate(self.STAGES)}, n.value
+
+    def stats(self, reset=True):
+        """(forwards, experts touched summed over forwards) since the last reset."""
+        f, u = U64(), U64()
+        _check(lib().hy3x_layer_stats(self._h, ctypes.byref(f), ctypes.byref(u), 1 if reset else 0))
+        return f.value, u.value
 
     def forward(self, x_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE, stream=None):
         """In-place MoE block on device memory x[T x 4096] (fp32)."""

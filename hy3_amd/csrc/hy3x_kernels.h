@@ -4,12 +4,17 @@
 
 namespace hy3x {
 
-__global__ void k_router_gemv(const float *x, const float *norm_w, const float *router,
-                              const float *bias, int has_bias, int K, float scale, float *logits,
-                              __half *s16, int32_t *ids, float *wpre, float *wout,
-                              unsigned *tickets);
+__global__ void k_router_small(const float *x, const float *norm_w, const float *router,
+                               const float *bias, int has_bias, int K, float scale, float *logits,
+                               __half *s16, float *s32, int32_t *ids, float *wpre, float *wout,
+                               unsigned *tickets);
+__global__ void k_rmsnorm(const float *x, const float *norm_w, __half *s16, float *s32);
+__global__ void k_router_gemm(const float *s32, const float *router, int T, float *logits);
+__global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
+                       int32_t *ids, float *wpre, float *wout);
 __global__ void k_dispatch(const int32_t *ids, int T, int K, int NT, int32_t *list, int4 *tiles,
-                           int32_t *n_tiles, int max_tiles, int32_t *counts_out);
+                           int32_t *n_tiles, int max_tiles, int32_t *counts_out,
+                           unsigned long long *stats);
 template <int NT>
 __global__ void k_gateup_gemv(const uint8_t *wq, const __half *s16, const int32_t *list,
                               const int4 *tiles, const int32_t *n_tiles, int T, int K,

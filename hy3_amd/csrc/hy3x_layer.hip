@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/hy3x_moe.h"
 #include "hy3x_kernels.h"
@@ -27,14 +28,34 @@ struct hy3x_layer {
   int has_bias = 0, router_set = 0;
   float *logits = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
   __half *s16 = nullptr, *h16 = nullptr;
+  float *s32 = nullptr;
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
   unsigned *tickets = nullptr;
+  unsigned long long *stats = nullptr;
   int max_tiles_alloc = 0;
   int last_T = 0, last_K = 0;
   hipStream_t last_stream = nullptr;
   int path = 0;
+  // per-kernel timing (diagnostics): events recorded around every stage
+  int timing = 0;
+  std::vector<hipEvent_t> ev_pool;
+  std::vector<int> ev_stage;  // stage of the interval that ends at event i (-1: start)
+  size_t ev_used = 0;
+  int n_timed = 0;
 };
+
+static int record_stage(hy3x_layer *L, hipStream_t st, int stage) {
+  if (!L->timing) return 0;
+  if (L->ev_used == L->ev_pool.size()) {
+    hipEvent_t ev;
+    if (hipEventCreate(&ev) != hipSuccess) return -1;
+    L->ev_pool.push_back(ev);
+    L->ev_stage.push_back(-1);
+  }
+  L->ev_stage[L->ev_used] = stage;
+  return hipEventRecord(L->ev_pool[L->ev_used++], st) == hipSuccess ? 0 : -1;
+}
 
 static thread_local std::string g_err;
 
@@ -67,6 +88,10 @@ static int dalloc(P **p, size_t bytes) {
   return HY3X_OK;
 }
 
+// Up to this many tokens the router runs as one wave per (expert, token);
+// above it as RMSNorm + LDS-tiled GEMM + per-token top-K.
+constexpr int kSmallRouterT = 8;
+
 static int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
   return n / NT + std::min(E, n) + (T + NT - 1) / NT + 1;
@@ -84,10 +109,11 @@ int hy3x_set_device(int device) {
 int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
   void *ptrs[] = {L->wq,   L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
-                  L->w,    L->out,    L->s16,    L->h16,     L->ids,     L->list,
-                  L->n_tiles, L->counts, L->tiles, L->tickets};
+                  L->w,    L->out,    L->s16, L->s32,    L->h16,     L->ids,     L->list,
+                  L->n_tiles, L->counts, L->tiles, L->tickets, L->stats};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
+  for (hipEvent_t ev : L->ev_pool) (void)hipEventDestroy(ev);
   delete L;
   return HY3X_OK;
 }
@@ -112,18 +138,21 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
       (rc = dalloc(&L->w, T * KMAX * sizeof(float))) ||
       (rc = dalloc(&L->ids, T * KMAX * sizeof(int32_t))) ||
       (rc = dalloc(&L->s16, T * D * sizeof(__half))) ||
+      (rc = dalloc(&L->s32, T * D * sizeof(float))) ||
       (rc = dalloc(&L->h16, slots * F * sizeof(__half))) ||
       (rc = dalloc(&L->out, slots * D * sizeof(float))) ||
       (rc = dalloc(&L->list, slots * sizeof(int32_t))) ||
       (rc = dalloc(&L->tiles, (size_t)L->max_tiles_alloc * sizeof(int4))) ||
       (rc = dalloc(&L->n_tiles, sizeof(int32_t))) ||
       (rc = dalloc(&L->counts, (E + 1) * sizeof(int32_t))) ||
-      (rc = dalloc(&L->tickets, T * sizeof(unsigned)))) {
+      (rc = dalloc(&L->tickets, T * sizeof(unsigned))) ||
+      (rc = dalloc(&L->stats, 2 * sizeof(unsigned long long)))) {
     hy3x_layer_destroy(L);
     return rc;
   }
   if (hipMemset(L->tickets, 0, T * sizeof(unsigned)) != hipSuccess ||
-      hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess) {
+      hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
+      hipMemset(L->stats, 0, 2 * sizeof(unsigned long long)) != hipSuccess) {
     hy3x_layer_destroy(L);
     return fail(HY3X_E_HIP, "hipMemset failed");
   }
@@ -174,28 +203,79 @@ int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void 
   if (K < 1 || K > KMAX) return fail(HY3X_E_ARG, "K=%d outside [1,8]", K);
   if (!L->router_set) return fail(HY3X_E_STATE, "router not set");
   hipStream_t st = (hipStream_t)stream;
-  k_router_gemv<<<dim3(E / 4, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias, L->has_bias, K,
-                                                 scale, L->logits, L->s16, L->ids, L->wpre, L->w,
-                                                 L->tickets);
+  record_stage(L, st, -1);
+  if (T <= kSmallRouterT) {
+    k_router_small<<<dim3(E, T), 64, 0, st>>>(x, L->norm_w, L->router, L->bias, L->has_bias, K,
+                                              scale, L->logits, L->s16, L->s32, L->ids, L->wpre,
+                                              L->w, L->tickets);
+  } else {
+    k_rmsnorm<<<T, 64, 0, st>>>(x, L->norm_w, L->s16, L->s32);
+    k_router_gemm<<<dim3((T + 31) / 32, E / 64), 256, 0, st>>>(L->s32, L->router, T, L->logits);
+    k_topk<<<T, 64, 0, st>>>(L->logits, L->bias, L->has_bias, K, scale, L->ids, L->wpre, L->w);
+  }
   const int NT = T == 1 ? 1 : 4;
   const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
-  k_dispatch<<<1, 1024, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts);
+  record_stage(L, st, HY3X_STAGE_ROUTER);
+  k_dispatch<<<1, 1024, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts,
+                                 L->stats);
+  record_stage(L, st, HY3X_STAGE_DISPATCH);
   if (NT == 1) {
     k_gateup_gemv<1><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
                                                     T, K, L->h16);
+    record_stage(L, st, HY3X_STAGE_GATEUP);
     k_down_gemv<1><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
                                                   L->out);
   } else {
     k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
                                                     T, K, L->h16);
+    record_stage(L, st, HY3X_STAGE_GATEUP);
     k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
                                                   L->out);
   }
+  record_stage(L, st, HY3X_STAGE_DOWN);
   k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+  record_stage(L, st, HY3X_STAGE_COMBINE);
+  if (L->timing) L->n_timed++;
   HIP_TRY(hipGetLastError());
   L->last_T = T;
   L->last_K = K;
   L->last_stream = st;
+  return HY3X_OK;
+}
+
+int hy3x_layer_set_timing(hy3x_layer *L, int enable) {
+  if (!L) return fail(HY3X_E_ARG, "NULL layer");
+  L->timing = enable ? 1 : 0;
+  L->ev_used = 0;
+  L->n_timed = 0;
+  return HY3X_OK;
+}
+
+int hy3x_layer_stage_times(hy3x_layer *L, float *ms, int n_stages, int *n_forwards) {
+  if (!L || !ms || n_stages < 1) return fail(HY3X_E_ARG, "bad argument");
+  for (int i = 0; i < n_stages; i++) ms[i] = 0.0f;
+  if (L->ev_used) HIP_TRY(hipEventSynchronize(L->ev_pool[L->ev_used - 1]));
+  for (size_t i = 1; i < L->ev_used; i++) {
+    const int stg = L->ev_stage[i];
+    if (stg < 0 || stg >= n_stages) continue;
+    float t = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&t, L->ev_pool[i - 1], L->ev_pool[i]));
+    ms[stg] += t;
+  }
+  if (n_forwards) *n_forwards = L->n_timed;
+  L->ev_used = 0;
+  L->n_timed = 0;
+  return HY3X_OK;
+}
+
+int hy3x_layer_stats(hy3x_layer *L, uint64_t *forwards, uint64_t *experts_touched, int reset) {
+  if (!L) return fail(HY3X_E_ARG, "NULL layer");
+  unsigned long long h[2];
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(h, L->stats, sizeof(h), hipMemcpyDeviceToHost));
+  if (forwards) *forwards = h[0];
+  if (experts_touched) *experts_touched = h[1];
+  if (reset) HIP_TRY(hipMemset(L->stats, 0, sizeof(h)));
   return HY3X_OK;
 }
 

@@ -54,6 +54,13 @@ __device__ __forceinline__ uint16_t fp32_to_fp16_trunc(float f) {
   return (uint16_t)((sign << 15) | ((uint32_t)ne << 10) | (man >> 13));
 }
 
+// (int)v as the reference's x86 build executes it: truncation, and INT_MIN
+// for NaN or values outside the int range (the GPU's own conversion would
+// saturate instead).
+__device__ __forceinline__ int cvt_trunc_x86(float v) {
+  return (v >= -2147483648.0f && v < 2147483648.0f) ? (int)v : (int)0x80000000u;
+}
+
 // One wave per Q4_K block; lane L holds elements 4L..4L+3 (sub-block L/8).
 // src == nullptr: generate the block of the whole-layer arena (193 experts x
 // gate|up|down, contiguous) from (seed, layer); otherwise quantise src.
@@ -94,7 +101,8 @@ __global__ __launch_bounds__(256) void k_synth_q4k(uint8_t *dst, int64_t nblocks
   if (max_m < 1e-10f) max_m = 1e-10f;
   const float d = max_s * inv63, dmin = max_m * inv63;
   const float rd = c63 / max_s, rdm = c63 / max_m;
-  int ls = (int)__builtin_fmaf(sub_scale, rd, 0.5f), lm = (int)__builtin_fmaf(sub_min, rdm, 0.5f);
+  int ls = cvt_trunc_x86(__builtin_fmaf(sub_scale, rd, 0.5f));
+  int lm = cvt_trunc_x86(__builtin_fmaf(sub_min, rdm, 0.5f));
   ls = ls < 0 ? 0 : (ls > 63 ? 63 : ls);
   lm = lm < 0 ? 0 : (lm > 63 ? 63 : lm);
   const float eff_d = d * (float)ls, eff_dm = dmin * (float)lm;
@@ -102,7 +110,7 @@ __global__ __launch_bounds__(256) void k_synth_q4k(uint8_t *dst, int64_t nblocks
   uint32_t packed = 0;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    int q = (int)__builtin_fmaf(v[c] + eff_dm, rq, 0.5f);
+    int q = cvt_trunc_x86(__builtin_fmaf(v[c] + eff_dm, rq, 0.5f));
     q = q < 0 ? 0 : (q > 15 ? 15 : q);
     packed |= (uint32_t)q << (8 * c);
   }

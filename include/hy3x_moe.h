@@ -97,6 +97,27 @@ int hy3x_layer_forward(hy3x_layer *layer, float *x, int T, int K, float scale, v
  * (before the scale), w[T x K] (after). Any pointer may be NULL. */
 int hy3x_layer_last_routing(hy3x_layer *layer, int32_t *ids, float *wpre, float *w);
 
+/* Per-stage timing (diagnostics, no counterpart in the reference beyond its
+ * HY3_TIMING wall clocks, hy3.c:1532-1563): while enabled, every forward
+ * records HIP events on its stream between its kernel stages.
+ * hy3x_layer_stage_times() synchronises, returns the accumulated milliseconds
+ * per stage (index HY3X_STAGE_*) and the number of forwards timed, and resets
+ * the accumulators. Enabling also resets. */
+#define HY3X_STAGE_ROUTER 0   /* RMSNorm + router GEMV + top-K        */
+#define HY3X_STAGE_DISPATCH 1 /* per-expert lists and work tiles      */
+#define HY3X_STAGE_GATEUP 2   /* gate/up GEMV or GEMM + SwiGLU         */
+#define HY3X_STAGE_DOWN 3     /* down GEMV or GEMM                     */
+#define HY3X_STAGE_COMBINE 4  /* weighted combine + residual           */
+#define HY3X_N_STAGES 8
+int hy3x_layer_set_timing(hy3x_layer *layer, int enable);
+int hy3x_layer_stage_times(hy3x_layer *layer, float *ms, int n_stages, int *n_forwards);
+
+/* Device-side counters since the last reset: forwards run and the sum over
+ * forwards of the experts touched (shared expert included), i.e. the "U" of
+ * the algorithmic byte count. Synchronises the device. */
+int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_touched,
+                     int reset);
+
 /* Execution-path override for tests: 0 = automatic (by T), 1 = force the
  * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path. */
 int hy3x_layer_set_path(hy3x_layer *layer, int path);

@@ -147,6 +147,14 @@ void hy3o_dequant_q4k(float *dst, const uint8_t *src, int64_t n) {
   }
 }
 
+/* (int)v as the reference's x86 build executes it (cvttss2si): truncation, and
+ * INT_MIN for NaN or anything outside the int range (C leaves that undefined;
+ * the quantiser reaches it for constant blocks, where 1/max(eff_d, 1e-10)
+ * scales values past 2^31). */
+static inline int cvt_trunc_x86(float v) {
+  return (v >= -2147483648.0f && v < 2147483648.0f) ? (int)v : (int)0x80000000u;
+}
+
 /* hy3_convert.c:605-651 as its Makefile builds it (-O3 -ffast-math): the
  * divisions by the constants 15 and 63 become multiplies by their rounded
  * reciprocals, 1/d is folded to 62.999996f/max_s, each remaining division v/d
@@ -186,7 +194,8 @@ static void quantize_block_q4k(const float *xb, uint8_t *out) {
   uint8_t *scales = out + 4;
   memset(scales, 0, 12);
   for (int j = 0; j < 8; j++) {
-    int ls = (int)fmaf(sub_scale[j], rd, 0.5f), lm = (int)fmaf(sub_min[j], rdm, 0.5f);
+    int ls = cvt_trunc_x86(fmaf(sub_scale[j], rd, 0.5f));
+    int lm = cvt_trunc_x86(fmaf(sub_min[j], rdm, 0.5f));
     if (ls < 0) ls = 0;
     if (ls > 63) ls = 63;
     if (lm < 0) lm = 0;
@@ -202,7 +211,7 @@ static void quantize_block_q4k(const float *xb, uint8_t *out) {
     const float eff_d = d * (float)ls, eff_dm = dmin * (float)lm;
     const float rq = 1.0f / (eff_d > 1e-10f ? eff_d : 1e-10f);
     for (int i = 0; i < 32; i++) {
-      int q = (int)fmaf(xb[32 * j + i] + eff_dm, rq, 0.5f);
+      int q = cvt_trunc_x86(fmaf(xb[32 * j + i] + eff_dm, rq, 0.5f));
       if (q < 0) q = 0;
       if (q > 15) q = 15;
       L[32 * j + i] = (uint8_t)q;
@@ -236,60 +245,71 @@ void hy3o_gen_q4k_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float s
 /* Routing contract                                                          */
 /* ======================================================================== */
 
-float hy3o_dot_lanes(const float *a, const float *b, int n) {
-  float p[64];
-  const int iters = n / 256;
-  for (int l = 0; l < 64; l++) {
-    float acc = 0.0f;
-    for (int i = 0; i < iters; i++)
-      for (int c = 0; c < 4; c++) {
-        const int j = 256 * i + 4 * l + c;
-        acc = fmaf(a[j], b[j], acc);
-      }
-    p[l] = acc;
-  }
-  for (int o = 32; o >= 1; o >>= 1) {
-    float q[64];
-    for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ o];
-    memcpy(p, q, sizeof(q));
-  }
-  return p[0];
+/* The reduction order the reference's build gives these sums (gcc -O3
+ * -ffast-math, 8-wide FMA vectors): eight chains, chain v accumulating
+ * a[8i+v]*b[8i+v] with fmaf for i ascending from 0, then the horizontal tree
+ * ((a1+a5)+(a3+a7)) + ((a0+a4)+(a2+a6)). */
+static float tree8(const float *a) {
+  const float t0 = a[0] + a[4], t1 = a[1] + a[5], t2 = a[2] + a[6], t3 = a[3] + a[7];
+  const float u0 = t2 + t0, u1 = t3 + t1;
+  return u1 + u0;
 }
 
-/* exp(x) by Cody-Waite reduction x = k*ln2 + r (two-part ln2) and a degree-7
- * Taylor polynomial for e^r on |r| <= ln2/2 (truncation error < 6e-9 relative),
- * scaled by 2^k built from the exponent bits. Used only inside the router's
- * sigmoid; inputs below -87 return 0 (1 + e^x rounds to 1 there anyway). */
-float hy3o_sig_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72f) return INFINITY;
-  if (x < -87.0f) return 0.0f;
-  const float kf = rintf(x * 1.44269502f);
-  float r = fmaf(kf, -0.693145751953125f, x);
-  r = fmaf(kf, -1.428606765330187e-06f, r);
-  float p = 1.98412701e-4f;               /* 1/7! */
-  p = fmaf(p, r, 1.38888892e-3f);          /* 1/6! */
-  p = fmaf(p, r, 8.33333377e-3f);          /* 1/5! */
-  p = fmaf(p, r, 4.16666679e-2f);          /* 1/4! */
-  p = fmaf(p, r, 1.66666672e-1f);          /* 1/3! */
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  const int k = (int)kf;
-  const int k1 = k / 2, k2 = k - k1;
-  uint32_t b1 = (uint32_t)(k1 + 127) << 23, b2 = (uint32_t)(k2 + 127) << 23;
-  float s1, s2;
-  memcpy(&s1, &b1, 4);
-  memcpy(&s2, &b2, 4);
-  return (p * s1) * s2;
+float hy3o_dot8(const float *a, const float *b, int n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < n / 8; i++)
+    for (int v = 0; v < 8; v++) acc[v] = fmaf(a[8 * i + v], b[8 * i + v], acc[v]);
+  return tree8(acc);
 }
 
-/* RMSNorm with the contract's reduction order; the per-element step follows
- * hy3.c:435-444: out = (x * r) * w with r = 1/sqrt(ss/n + eps). */
+/* exp(x) rounded to fp32 from a double-precision evaluation: Cody-Waite
+ * reduction x = k*ln2 + r (two-part ln2 in double), a degree-13 Taylor
+ * polynomial for e^r (|r| <= 0.35, truncation < 1e-17 relative) and exact
+ * scaling by 2^k. The double result is within a few ulp(double) of e^x, so the
+ * final rounding gives the correctly rounded float except in cases closer to a
+ * rounding boundary than ~1e-15 relative. Used only for the router sigmoid;
+ * inputs below -87 return 0 (1 + e^x rounds to 1 there anyway). */
+float hy3o_sig_expf(float xf) {
+  if (xf != xf) return xf;
+  if (xf > 88.72f) return INFINITY;
+  if (xf < -87.0f) return 0.0f;
+  const double x = (double)xf;
+  const double kd = rint(x * 1.4426950408889634);
+  double r = fma(kd, -6.93147180369123816490e-01, x);
+  r = fma(kd, -1.90821492927058770002e-10, r);
+  double p = 1.0 / 6227020800.0;
+  p = fma(p, r, 1.0 / 479001600.0);
+  p = fma(p, r, 1.0 / 39916800.0);
+  p = fma(p, r, 1.0 / 3628800.0);
+  p = fma(p, r, 1.0 / 362880.0);
+  p = fma(p, r, 1.0 / 40320.0);
+  p = fma(p, r, 1.0 / 5040.0);
+  p = fma(p, r, 1.0 / 720.0);
+  p = fma(p, r, 1.0 / 120.0);
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  const int64_t k = (int64_t)kd;
+  uint64_t bits = (uint64_t)(k + 1023) << 52;
+  double s;
+  memcpy(&s, &bits, 8);
+  return (float)(p * s);
+}
+
+/* RMSNorm (hy3.c:435-444) as built: ss in the 8-chain order, r = 1/sqrt(ss/n
+ * + eps) correctly rounded (the build uses an rsqrt estimate refined by one
+ * Newton step, whose last bit depends on the host CPU), out = (x * w) * r (the
+ * build's reassociation of x * r * w). */
+static float rms_scale(const float *x, int n) {
+  const float ss = hy3o_dot8(x, x, n);
+  return 1.0f / sqrtf(ss / (float)n + HY3O_RMS_EPS);
+}
+
 void hy3o_rms_norm(float *out, const float *x, const float *w, int n) {
-  const float ss = hy3o_dot_lanes(x, x, n);
-  const float r = 1.0f / sqrtf(ss / (float)n + HY3O_RMS_EPS);
-  for (int i = 0; i < n; i++) out[i] = x[i] * r * w[i];
+  const float r = rms_scale(x, n);
+  for (int i = 0; i < n; i++) out[i] = (x[i] * w[i]) * r;
 }
 
 /* hy3.c:654-666. */
@@ -313,16 +333,18 @@ void hy3o_topk_select(float *vals, int *inds, const float *scores, int n, int k)
   }
 }
 
-/* hy3.c:1266-1291 (routing half of the MoE block). */
-void hy3o_route_token(const float *x, const float *norm_w, const float *router,
-                      const float *bias, int has_bias, int K, float scale,
-                      float *s_out, float *logits, float *sigm, float *score,
-                      int32_t *ids, float *wpre, float *w) {
+/* hy3.c:1266-1291 (routing half of the MoE block). r_override > 0 replaces
+ * the RMSNorm scale (test hook: feed the reference build's own r). */
+void hy3o_route_token_r(const float *x, const float *norm_w, const float *router,
+                        const float *bias, int has_bias, int K, float scale, float r_override,
+                        float *s_out, float *logits, float *sigm, float *score,
+                        int32_t *ids, float *wpre, float *w) {
   float s[HY3O_D], lg[HY3O_E], sg[HY3O_E], sc[HY3O_E], tv[HY3O_KMAX];
   int ti[HY3O_KMAX];
-  hy3o_rms_norm(s, x, norm_w, HY3O_D);
+  const float r = r_override > 0.0f ? r_override : rms_scale(x, HY3O_D);
+  for (int i = 0; i < HY3O_D; i++) s[i] = (x[i] * norm_w[i]) * r;
   for (int e = 0; e < HY3O_E; e++) {
-    lg[e] = hy3o_dot_lanes(router + (size_t)e * HY3O_D, s, HY3O_D);
+    lg[e] = hy3o_dot8(router + (size_t)e * HY3O_D, s, HY3O_D);
     sg[e] = 1.0f / (1.0f + hy3o_sig_expf(-lg[e]));
     sc[e] = sg[e];
     if (has_bias && bias) sc[e] += bias[e];
@@ -341,6 +363,14 @@ void hy3o_route_token(const float *x, const float *norm_w, const float *router,
   if (logits) memcpy(logits, lg, sizeof(lg));
   if (sigm) memcpy(sigm, sg, sizeof(sg));
   if (score) memcpy(score, sc, sizeof(sc));
+}
+
+void hy3o_route_token(const float *x, const float *norm_w, const float *router,
+                      const float *bias, int has_bias, int K, float scale, float *s_out,
+                      float *logits, float *sigm, float *score, int32_t *ids, float *wpre,
+                      float *w) {
+  hy3o_route_token_r(x, norm_w, router, bias, has_bias, K, scale, 0.0f, s_out, logits, sigm,
+                     score, ids, wpre, w);
 }
 
 /* ======================================================================== */

@@ -69,10 +69,9 @@ void hy3o_quantize_q4k(const float *x, uint8_t *dst, int64_t n);           /* hy
 void hy3o_gen_q4k_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float sigma);
 
 /* ---- routing contract --------------------------------------------------- */
-/* Fixed-order fp32 dot product over n = 4096 (any multiple of 256): 64 lanes,
- * lane l accumulates a[256i+4l+c]*b[...] by fmaf over (i, c) in lexicographic
- * order from 0, then an xor-butterfly over the lanes (offsets 32..1). */
-float hy3o_dot_lanes(const float *a, const float *b, int n);
+/* Fixed-order fp32 dot product (n a multiple of 8): eight fmaf chains over
+ * j = 8i+v, then ((a1+a5)+(a3+a7)) + ((a0+a4)+(a2+a6)). */
+float hy3o_dot8(const float *a, const float *b, int n);
 float hy3o_sig_expf(float x);                 /* exp for the router sigmoid */
 void hy3o_rms_norm(float *out, const float *x, const float *w, int n);
 /* Full routing for one token: s (normalised input) is written to s_out if
@@ -82,6 +81,10 @@ void hy3o_route_token(const float *x, const float *norm_w, const float *router,
                       const float *bias, int has_bias, int K, float scale,
                       float *s_out, float *logits, float *sigm, float *score,
                       int32_t *ids, float *wpre, float *w);
+void hy3o_route_token_r(const float *x, const float *norm_w, const float *router,
+                        const float *bias, int has_bias, int K, float scale, float r_override,
+                        float *s_out, float *logits, float *sigm, float *score,
+                        int32_t *ids, float *wpre, float *w);
 /* Selection sort with swaps, strict '>' (hy3.c:654-666). */
 void hy3o_topk_select(float *vals, int *inds, const float *scores, int n, int k);
 

@@ -37,10 +37,11 @@ _SIGS = {
     "hy3o_dequant_q4k": (None, [P, P, I64]),
     "hy3o_quantize_q4k": (None, [P, P, I64]),
     "hy3o_gen_q4k_matrix": (None, [P, I32, I32, U64, F32]),
-    "hy3o_dot_lanes": (F32, [P, P, I32]),
+    "hy3o_dot8": (F32, [P, P, I32]),
     "hy3o_sig_expf": (F32, [F32]),
     "hy3o_rms_norm": (None, [P, P, P, I32]),
     "hy3o_route_token": (None, [P, P, P, P, I32, I32, F32, P, P, P, P, P, P, P]),
+    "hy3o_route_token_r": (None, [P, P, P, P, I32, I32, F32, F32, P, P, P, P, P, P, P]),
     "hy3o_topk_select": (None, [P, P, P, I32, I32]),
     "hy3o_mul_mat_q4k": (None, [P, P, P, I32, I32]),
     "hy3o_moe_token": (None, [P, P, I32, F32, P, P, P]),
@@ -59,6 +60,8 @@ _REF_SIGS = {
     "hy3ref_moe_forward": (I32, [P, I32, I32, P, P, P, I32, P, P, P, P, I32]),
     "hy3ref_quantize_q4k": (None, [P, P, I32]),
     "hy3ref_fp32_to_fp16": (ctypes.c_uint16, [F32]),
+    "hy3ref_rms_r": (F32, [P, I32]),
+    "hy3ref_router_scores": (None, [P, P, P, P, I32, P, P, P]),
 }
 
 _lib = None
@@ -178,8 +181,9 @@ class SynthLayer:
             s.gate[e], s.up[e], s.down[e] = g.ctypes.data, u.ctypes.data, d.ctypes.data
         return s
 
-    def route(self, x, K=8, scale=2.826):
-        """Routing contract for each row of x: ids, wpre, w, plus s/logits/sigmoid/score."""
+    def route(self, x, K=8, scale=2.826, r_override=None):
+        """Routing contract for each row of x: ids, wpre, w, plus s/logits/sigmoid/score.
+        r_override[t] > 0 replaces the RMSNorm scale of token t (test hook)."""
         x = np.ascontiguousarray(x, np.float32).reshape(-1, D)
         T = x.shape[0]
         ids = np.zeros((T, K), np.int32)
@@ -191,11 +195,12 @@ class SynthLayer:
         sc = np.zeros((T, E), np.float32)
         L = lib()
         for t in range(T):
-            L.hy3o_route_token(x[t].ctypes.data, self.norm_w.ctypes.data, self.router.ctypes.data,
-                               self.bias.ctypes.data, 1 if self.has_bias else 0, K, scale,
-                               s[t].ctypes.data, lg[t].ctypes.data, sg[t].ctypes.data,
-                               sc[t].ctypes.data, ids[t].ctypes.data, wpre[t].ctypes.data,
-                               w[t].ctypes.data)
+            r = 0.0 if r_override is None else float(r_override[t])
+            L.hy3o_route_token_r(x[t].ctypes.data, self.norm_w.ctypes.data,
+                                 self.router.ctypes.data, self.bias.ctypes.data,
+                                 1 if self.has_bias else 0, K, scale, r, s[t].ctypes.data,
+                                 lg[t].ctypes.data, sg[t].ctypes.data, sc[t].ctypes.data,
+                                 ids[t].ctypes.data, wpre[t].ctypes.data, w[t].ctypes.data)
         return dict(ids=ids, wpre=wpre, w=w, s=s, logits=lg, sigmoid=sg, score=sc)
 
     def forward(self, x, K=8, scale=2.826):

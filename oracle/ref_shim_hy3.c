@@ -28,6 +28,33 @@ void hy3ref_mul_mat(float *dst, const uint8_t *w, uint32_t type, const float *x,
 }
 void hy3ref_set_threads(int n) { omp_set_num_threads(n); }
 
+/* The RMSNorm scale r = 1/sqrt(mean(x^2) + eps) as the reference build
+ * computes it (hy3.c:435-439: an rsqrt estimate plus one Newton step under
+ * -ffast-math, so the last bits depend on the host CPU). */
+float hy3ref_rms_r(const float *x, int n) { return rms_norm_val(x, n, HY3_RMS_EPS); }
+
+/* hy3.c:1266-1277 through the reference's own static helpers: s = rms_norm,
+ * logits = mul_mat_f32 (F32 router), scores = sigmoid (+ bias). Used to check
+ * that hy3ref_rms_r sees the same arithmetic as forward_layer_moe. */
+/* The sigmoid loop of forward_layer_moe compiles to scalar expf calls and an
+ * exact division; keep this copy scalar too (a plain loop would be vectorised
+ * with vector expf and reciprocal estimates). */
+__attribute__((optimize("no-tree-vectorize"))) static void shim_sigmoid(
+    const float *logits, const float *bias, int has_bias, float *scores) {
+  for (int i = 0; i < HY3_N_EXPERT; i++) {
+    float sg = 1.0f / (1.0f + expf(-logits[i]));
+    scores[i] = has_bias ? sg + bias[i] : sg;
+  }
+}
+
+void hy3ref_router_scores(const float *x, const float *norm_w, const float *router,
+                          const float *bias, int has_bias, float *s_out, float *logits,
+                          float *scores) {
+  rms_norm(s_out, x, norm_w, HY3_N_EMBD, HY3_RMS_EPS);
+  mul_mat_f32(logits, (const uint8_t *)router, 0, s_out, HY3_N_EXPERT, HY3_N_EMBD);
+  shim_sigmoid(logits, bias, has_bias, scores);
+}
+
 static hy3_tensor_info ti_f32 = {0}, ti_q4k = {0}, ti_none = {0};
 
 /* x: [T x 4096] updated in place. gate/up/down: 193 host pointers each (index

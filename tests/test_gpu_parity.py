@@ -1,0 +1,252 @@
+"""HIP path (libhy3x.so through its C ABI) against the CPU oracle and the
+reference fixtures. Needs an MI355X: marked gpu.
+
+Bars: routing bit-exact against the oracle (ids identical, pre-scale weights
+bit-identical); against hy3.c's fixtures ids identical and pre-scale weights
+within 8 ulp (the reference's RMSNorm scale comes from the host CPU's rsqrt
+estimate); MoE output relative L2 <= 1e-3 on the delta y - x and on y.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import hy3_amd as H
+from hy3_amd import configs as C
+from hy3_amd import hipmem
+from oracle import hy3_oracle as O
+
+pytestmark = pytest.mark.gpu
+G = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+D, E = 4096, 192
+TOL = 1e-3
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def ulp_dist(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "no GPU"
+    return t
+
+
+@pytest.fixture(scope="module")
+def layer(torch):
+    L = H.MoELayer(4096)
+    L.synth_experts(C.WEIGHT_SEED, 0)
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    L.set_router(nw, rt, b)
+    yield L
+    L.close()
+
+
+class DeviceBackedLayer(O.SynthLayer):
+    """Oracle layer whose expert bytes are copied from the device arena."""
+
+    def __init__(self, dev_layer, seed, layer=0):
+        super().__init__(seed, layer)
+        self.dev = dev_layer
+
+    def expert(self, e):
+        if e not in self.experts:
+            self.experts[e] = tuple(hipmem.to_host(self.dev.expert_ptr(e, m), H.Q4K_MATRIX_BYTES)
+                                    for m in range(3))
+        return self.experts[e]
+
+
+@pytest.fixture(scope="module")
+def cpu(layer):
+    return DeviceBackedLayer(layer, C.WEIGHT_SEED)
+
+
+def set_bias(layer, cpu, kind, seed=None):
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    if kind == "zipf":
+        b = H.synth_zipf_bias(E, seed)
+    layer.set_router(nw, rt, None if kind == "none" else b)
+    cpu.bias = b.copy()
+    cpu.has_bias = kind != "none"
+
+
+def run(torch, layer, x, K=8):
+    T = x.shape[0]
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).copy()).cuda()
+    layer.forward(xd.data_ptr(), T, K)
+    torch.cuda.synchronize()
+    ids, wpre, w = layer.last_routing(T, K)
+    return xd.cpu().numpy(), ids, wpre, w
+
+
+# ---------------------------------------------------------------- inputs
+def test_synth_layer_matches_reference_quantiser(layer):
+    """The device generator + quantiser reproduce, for all 579 matrices of the
+    layer, the bytes hy3_convert.c's compiled quantize_row_q4_K wrote."""
+    with open(os.path.join(G, "layer.json")) as f:
+        meta = json.load(f)
+    bad = []
+    for e in range(E + 1):
+        got = [sha(hipmem.to_host(layer.expert_ptr(e, m), H.Q4K_MATRIX_BYTES)) for m in range(3)]
+        if got != meta["expert_sha256"][str(e)]:
+            bad.append(e)
+    assert not bad, f"experts differing from the reference quantiser: {bad}"
+
+
+def test_small_tensors_match_oracle():
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    ref = O.SynthLayer(C.WEIGHT_SEED)
+    assert np.array_equal(nw, ref.norm_w) and np.array_equal(rt.ravel(), ref.router)
+    assert np.array_equal(b, ref.bias)
+    assert np.array_equal(H.synth_zipf_bias(E, 0xC3), O.zipf_bias(E, 0xC3))
+    assert np.array_equal(C.inputs(0xC1, 3, first_token=5).ravel(),
+                          O.normal(3 * D, O.key(0xC1, 0, O.T_X), 1.0, first=5 * D))
+
+
+def test_device_quantiser_edge_blocks(torch):
+    f = np.load(os.path.join(G, "q4k_quant.npz"))
+    x = torch.from_numpy(f["x"]).cuda()
+    q = torch.zeros(f["q"].size, dtype=torch.uint8, device="cuda")
+    rc = H.lib().hy3x_synth_quantize_q4k(x.data_ptr(), q.data_ptr(), x.numel(), None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    got = q.cpu().numpy().reshape(-1, 144)
+    bad = np.nonzero((got != f["q"].reshape(-1, 144)).any(1))[0]
+    assert bad.size == 0, f"blocks differing: {bad.tolist()}"
+
+
+# ---------------------------------------------------------------- routing
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
+def test_routing_bit_exact_vs_oracle(torch, layer, cpu, cfg):
+    c = C.CONFIGS[cfg]
+    set_bias(layer, cpu, "zipf" if c.zipf_bias else "uniform", c.input_seed)
+    x = C.inputs(c.input_seed, c.T)
+    _, ids, wpre, w = run(torch, layer, x)
+    r = cpu.route(x)
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
+    assert np.array_equal(w.view(np.uint32), r["w"].view(np.uint32))
+    set_bias(layer, cpu, "uniform")
+
+
+@pytest.mark.parametrize("K", [1, 2, 4, 8])
+@pytest.mark.parametrize("T", [1, 5, 16])
+def test_routing_top_k_variants(torch, layer, cpu, K, T):
+    x = C.inputs(0xC2, T, first_token=100)
+    _, ids, wpre, _ = run(torch, layer, x, K)
+    r = cpu.route(x, K)
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
+
+
+def test_routing_without_bias(torch, layer, cpu):
+    set_bias(layer, cpu, "none")
+    x = C.inputs(0xC1, 12)
+    _, ids, wpre, _ = run(torch, layer, x)
+    r = cpu.route(x)
+    set_bias(layer, cpu, "uniform")
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
+
+
+# ---------------------------------------------------------------- outputs
+@pytest.mark.parametrize("cfg,sample", [(0, None), (1, None), (2, 8), (3, 8)])
+def test_output_vs_oracle(torch, layer, cpu, cfg, sample):
+    c = C.CONFIGS[cfg]
+    set_bias(layer, cpu, "zipf" if c.zipf_bias else "uniform", c.input_seed)
+    x = C.inputs(c.input_seed, c.T)
+    y, ids, _, _ = run(torch, layer, x)
+    rows = np.arange(c.T) if sample is None else np.linspace(0, c.T - 1, sample).astype(int)
+    yo, ro = cpu.forward(x[rows])
+    set_bias(layer, cpu, "uniform")
+    assert np.array_equal(ro["ids"], ids[rows])
+    assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL
+    assert O.rel_l2(y[rows], yo) <= TOL
+
+
+MOE_CASES = ["c0", "c0_k4", "c0_nobias", "c1", "c2", "c3"]
+
+
+@pytest.mark.parametrize("name", MOE_CASES)
+def test_vs_reference_fixtures(torch, layer, cpu, name):
+    f = np.load(os.path.join(G, "moe.npz"))
+    bk = str(f[f"{name}/bias_kind"][0])
+    seed = int(f[f"{name}/x_seed"][0])
+    ids_ref = f[f"{name}/ids"]
+    T, K = ids_ref.shape
+    set_bias(layer, cpu, bk, seed)
+    x = C.inputs(seed, T)
+    y, ids, wpre, _ = run(torch, layer, x, K)
+    set_bias(layer, cpu, "uniform")
+    assert np.array_equal(ids, ids_ref)
+    sig = f[f"{name}/sigmoid"]
+    sel = sig[np.arange(T)[:, None], ids_ref]
+    s = np.zeros(T, np.float32)
+    for k in range(K):
+        s = (s + sel[:, k]).astype(np.float32)
+    wref = (sel * (np.float32(1) / (s + np.float32(1e-20)))[:, None]).astype(np.float32)
+    assert ulp_dist(wpre, wref).max() <= 8
+    y_ref = f[f"{name}/y"]
+    n = y_ref.shape[0]
+    assert O.rel_l2(y[:n] - x[:n], y_ref - x[:n]) <= TOL
+    assert O.rel_l2(y[:n], y_ref) <= TOL
+
+
+def test_deterministic(torch, layer):
+    x = C.inputs(0xC2, 64)
+    y1, *_ = run(torch, layer, x)
+    y2, *_ = run(torch, layer, x)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+def test_zero_experts_leave_residual_unchanged(torch):
+    """Full-size property: all-zero Q4_K blocks dequantise to 0 (scales and
+    mins are 0; d decodes to 2^-15 by the fp16 quirk), so y == x exactly."""
+    L = H.MoELayer(512)
+    z = np.zeros(H.Q4K_MATRIX_BYTES, np.uint8)
+    for e in range(E + 1):
+        L.set_expert_q4k(e, z, z, z)
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    L.set_router(nw, rt, b)
+    x = C.inputs(0xC2, 512)
+    y, *_ = run(torch, L, x)
+    L.close()
+    assert np.array_equal(y.view(np.uint32), x.view(np.uint32))
+
+
+def test_stack_routing_per_layer(torch):
+    """Config 4 shape on a 4-layer stack: per-layer routing bit-exact."""
+    n = 4
+    layers, cpus = [], []
+    for li in range(n):
+        L = H.MoELayer(1)
+        L.synth_experts(0xC4, li)
+        nw, rt, b = C.layer_small_tensors(0xC4, li)
+        L.set_router(nw, rt, b)
+        layers.append(L)
+        cpus.append(DeviceBackedLayer(L, 0xC4, li))
+    x = C.inputs(0xC4, 1)
+    xd = torch.from_numpy(x.copy()).cuda()
+    xc = x.copy()
+    for li in range(n):
+        layers[li].forward(xd.data_ptr(), 1)
+        ids, wpre, _ = layers[li].last_routing(1, 8)
+        yc, rc = cpus[li].forward(xc)
+        assert np.array_equal(ids, rc["ids"]), li
+        assert np.array_equal(wpre.view(np.uint32), rc["wpre"].view(np.uint32)), li
+        # the GPU's y feeds the next layer on both sides (routing stays exact)
+        xc = xd.cpu().numpy()
+        assert O.rel_l2(xc, yc) <= TOL
+    for L in layers:
+        L.close()
