@@ -54,6 +54,7 @@ _SIGS = {
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
     "hy3x_layer_set_timing": (I32, [P, I32]),
+    "hy3x_layer_set_trace": (I32, [P, I32, P]),
     "hy3x_layer_stats": (I32, [P, ctypes.POINTER(U64), ctypes.POINTER(U64), I32]),
     "hy3x_layer_stage_times": (I32, [P, P, I32, ctypes.POINTER(I32)]),
     "hy3x_synth_layer_experts": (I32, [P, U64, U32]),

@@ -41,6 +41,15 @@ __host__ __device__ __forceinline__ int stage_index(int i) {
   return g * 64 + 2 * (4 * j + hi + ((e & 1) << 1)) + (e >> 1);
 }
 
+// Position of element k inside its run of 8 in the MFMA-staged fp16 layout:
+// the run holds k order (0,2,1,3,4,6,5,7), the order the nibble unpack of the
+// Q4_K bytes produces.
+__host__ __device__ __forceinline__ int perm8(int k) {
+  const int lo = k & 7;
+  const int p = lo == 1 ? 2 : lo == 2 ? 1 : lo == 5 ? 6 : lo == 6 ? 5 : lo;
+  return (k & ~7) | p;
+}
+
 // 64-lane xor-butterfly sum (every lane ends with the total). The addition
 // order is fixed: v_l += v_{l^o} for o = 32, 16, 8, 4, 2, 1.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -54,6 +63,63 @@ __device__ __forceinline__ float half_sum(float v) {
 #pragma unroll
   for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// DPP moves (gfx9 encodings): quad_perm [1,0,3,2] / [2,3,0,1], row_half_mirror,
+// row_mirror, row_bcast:15, row_bcast:31.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140,
+              DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// Sum over each row of 16 lanes; every lane of the row receives the row sum:
+// v += xor1, v += xor2, v += half-mirror (lane i <-> 7-i in each 8), v +=
+// mirror (i <-> 15-i in each 16), in that fixed order.
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma clang fp contract(off)
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  v += dpp<DPP_MIRROR>(v);
+  return v;
+}
+
+// Sum over the 64 lanes, returned as a wave-uniform value.
+__device__ __forceinline__ float wave_total(float v) {
+  v = row16_sum(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+}
+
+// Sums over each 32-lane half: .x = lanes 0..31, .y = lanes 32..63 (uniform).
+__device__ __forceinline__ float2 half_totals(float v) {
+  v = row16_sum(v);
+  const int b = __builtin_bit_cast(int, v);
+  return make_float2(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+                         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+                         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
+// Optional per-block timestamps for diagnostics (REALTIME counter, 100 MHz):
+// when trace_buf is non-null, thread 0 of block b writes checkpoint i to
+// trace_buf[b * 8 + i].
+__device__ __forceinline__ void trace_point(unsigned long long *trace_buf, int i) {
+  if (trace_buf && threadIdx.x == 0) {
+    const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+    __hip_atomic_store(&trace_buf[blockIdx.x * 8 + i], t, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }

@@ -4,10 +4,10 @@
 
 namespace hy3x {
 
-__global__ void k_router_small(const float *x, const float *norm_w, const float *router,
-                               const float *bias, int has_bias, int K, float scale, float *logits,
-                               __half *s16, float *s32, int32_t *ids, float *wpre, float *wout,
-                               unsigned *tickets);
+__global__ void k_router_logits(const float *x, const float *norm_w, const float *router,
+                                const float *bias, int has_bias, float *logits, float *sig,
+                                float *score, __half *s16, float *s32,
+                                unsigned long long *trace);
 __global__ void k_rmsnorm(const float *x, const float *norm_w, __half *s16, float *s32);
 __global__ void k_router_gemm(const float *s32, const float *router, int T, float *logits);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
@@ -22,6 +22,12 @@ __global__ void k_gateup_gemv(const uint8_t *wq, const __half *s16, const int32_
 template <int NT>
 __global__ void k_down_gemv(const uint8_t *wq, const __half *h16, const int32_t *list,
                             const int4 *tiles, const int32_t *n_tiles, float *out);
+__global__ void k_gateup_decode(const uint8_t *wq, const __half *s16, const float *sig,
+                                const float *score, int K, float scale, int32_t *ids,
+                                float *wpre, float *wout, unsigned long long *stats,
+                                __half *h16, unsigned long long *trace);
+__global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *ids,
+                              const float *w, int K, float *x, unsigned long long *trace);
 __global__ void k_combine(float *x, const float *out, const float *w, int T, int K);
 
 extern template __global__ void k_gateup_gemv<1>(const uint8_t *, const __half *, const int32_t *,
@@ -34,6 +40,18 @@ extern template __global__ void k_down_gemv<1>(const uint8_t *, const __half *, 
                                                const int4 *, const int32_t *, float *);
 extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, const int32_t *,
                                                const int4 *, const int32_t *, float *);
+
+template <bool GATEUP>
+__global__ void k_moe_mfma(const uint8_t *wq, const __half *act, const int32_t *list,
+                           const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m,
+                           float *out);
+extern template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const int32_t *,
+                                                 const int4 *, const int32_t *, int, int,
+                                                 __half *, float *);
+extern template __global__ void k_moe_mfma<false>(const uint8_t *, const __half *,
+                                                  const int32_t *, const int4 *, const int32_t *,
+                                                  int, int, __half *, float *);
+__global__ void k_stage_mfma(const float *s32, __half *s16m);
 
 __global__ void k_synth_q4k(uint8_t *dst, int64_t nblocks, uint64_t seed, uint32_t layer,
                             const float *src);

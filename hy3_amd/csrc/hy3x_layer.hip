@@ -26,8 +26,8 @@ struct hy3x_layer {
   uint8_t *wq = nullptr;
   float *norm_w = nullptr, *router = nullptr, *bias = nullptr;
   int has_bias = 0, router_set = 0;
-  float *logits = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
-  __half *s16 = nullptr, *h16 = nullptr;
+  float *logits = nullptr, *sig = nullptr, *score = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
+  __half *s16 = nullptr, *h16 = nullptr, *s16m = nullptr, *h16m = nullptr;
   float *s32 = nullptr;
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
@@ -37,6 +37,7 @@ struct hy3x_layer {
   int last_T = 0, last_K = 0;
   hipStream_t last_stream = nullptr;
   int path = 0;
+  unsigned long long *trace[3] = {nullptr, nullptr, nullptr};
   // per-kernel timing (diagnostics): events recorded around every stage
   int timing = 0;
   std::vector<hipEvent_t> ev_pool;
@@ -91,6 +92,9 @@ static int dalloc(P **p, size_t bytes) {
 // Up to this many tokens the router runs as one wave per (expert, token);
 // above it as RMSNorm + LDS-tiled GEMM + per-token top-K.
 constexpr int kSmallRouterT = 8;
+// From this many tokens the experts run as MFMA grouped GEMMs, below it as
+// wavefront-reduction GEMVs.
+constexpr int kMfmaMinT = 64;
 
 static int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
@@ -108,8 +112,8 @@ int hy3x_set_device(int device) {
 
 int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
-  void *ptrs[] = {L->wq,   L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
-                  L->w,    L->out,    L->s16, L->s32,    L->h16,     L->ids,     L->list,
+  void *ptrs[] = {L->wq, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
+                  L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m,    L->h16,     L->ids,     L->list,
                   L->n_tiles, L->counts, L->tiles, L->tickets, L->stats};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
@@ -134,11 +138,15 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
       (rc = dalloc(&L->router, (size_t)E * D * sizeof(float))) ||
       (rc = dalloc(&L->bias, E * sizeof(float))) ||
       (rc = dalloc(&L->logits, T * E * sizeof(float))) ||
+      (rc = dalloc(&L->sig, T * E * sizeof(float))) ||
+      (rc = dalloc(&L->score, T * E * sizeof(float))) ||
       (rc = dalloc(&L->wpre, T * KMAX * sizeof(float))) ||
       (rc = dalloc(&L->w, T * KMAX * sizeof(float))) ||
       (rc = dalloc(&L->ids, T * KMAX * sizeof(int32_t))) ||
       (rc = dalloc(&L->s16, T * D * sizeof(__half))) ||
       (rc = dalloc(&L->s32, T * D * sizeof(float))) ||
+      (rc = dalloc(&L->s16m, T * D * sizeof(__half))) ||
+      (rc = dalloc(&L->h16m, slots * F * sizeof(__half))) ||
       (rc = dalloc(&L->h16, slots * F * sizeof(__half))) ||
       (rc = dalloc(&L->out, slots * D * sizeof(float))) ||
       (rc = dalloc(&L->list, slots * sizeof(int32_t))) ||
@@ -204,37 +212,56 @@ int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void 
   if (!L->router_set) return fail(HY3X_E_STATE, "router not set");
   hipStream_t st = (hipStream_t)stream;
   record_stage(L, st, -1);
+  const bool decode = T == 1 && L->path == 0;
+  const bool use_mfma = L->path == 2 || (L->path == 0 && T >= kMfmaMinT);
   if (T <= kSmallRouterT) {
-    k_router_small<<<dim3(E, T), 64, 0, st>>>(x, L->norm_w, L->router, L->bias, L->has_bias, K,
-                                              scale, L->logits, L->s16, L->s32, L->ids, L->wpre,
-                                              L->w, L->tickets);
+    k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias, L->has_bias,
+                                                L->logits, L->sig, L->score, L->s16, L->s32,
+                                                L->trace[0]);
   } else {
-    k_rmsnorm<<<T, 64, 0, st>>>(x, L->norm_w, L->s16, L->s32);
+    k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, L->s16, L->s32);
     k_router_gemm<<<dim3((T + 31) / 32, E / 64), 256, 0, st>>>(L->s32, L->router, T, L->logits);
-    k_topk<<<T, 64, 0, st>>>(L->logits, L->bias, L->has_bias, K, scale, L->ids, L->wpre, L->w);
   }
-  const int NT = T == 1 ? 1 : 4;
-  const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
+  if (!decode)
+    k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, scale, L->ids, L->wpre, L->w);
   record_stage(L, st, HY3X_STAGE_ROUTER);
-  k_dispatch<<<1, 1024, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts,
-                                 L->stats);
-  record_stage(L, st, HY3X_STAGE_DISPATCH);
-  if (NT == 1) {
-    k_gateup_gemv<1><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
-                                                    T, K, L->h16);
+  if (decode) {
+    k_gateup_decode<<<(K + 1) * (F / 32), 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
+                                                        scale, L->ids, L->wpre,
+                                                        L->w, L->stats, L->h16, L->trace[1]);
     record_stage(L, st, HY3X_STAGE_GATEUP);
-    k_down_gemv<1><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
-                                                  L->out);
+    k_down_decode<<<D / 16, 576, 0, st>>>(L->wq, L->h16, L->ids, L->w, K, x, L->trace[2]);
+    record_stage(L, st, HY3X_STAGE_DOWN);
+  } else if (use_mfma) {
+    const int NT = 64;
+    const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
+    k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m);
+    k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts,
+                                  L->stats);
+    record_stage(L, st, HY3X_STAGE_DISPATCH);
+    k_moe_mfma<true><<<mt * (F / 64), 256, 0, st>>>(L->wq, L->s16m, L->list, L->tiles,
+                                                    L->n_tiles, T, K, L->h16m, nullptr);
+    record_stage(L, st, HY3X_STAGE_GATEUP);
+    k_moe_mfma<false><<<mt * (D / 64), 256, 0, st>>>(L->wq, L->h16m, L->list, L->tiles,
+                                                     L->n_tiles, T, K, nullptr, L->out);
+    record_stage(L, st, HY3X_STAGE_DOWN);
+    k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+    record_stage(L, st, HY3X_STAGE_COMBINE);
   } else {
+    const int NT = 4;
+    const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
+    k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts,
+                                  L->stats);
+    record_stage(L, st, HY3X_STAGE_DISPATCH);
     k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
                                                     T, K, L->h16);
     record_stage(L, st, HY3X_STAGE_GATEUP);
     k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
                                                   L->out);
+    record_stage(L, st, HY3X_STAGE_DOWN);
+    k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+    record_stage(L, st, HY3X_STAGE_COMBINE);
   }
-  record_stage(L, st, HY3X_STAGE_DOWN);
-  k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
-  record_stage(L, st, HY3X_STAGE_COMBINE);
   if (L->timing) L->n_timed++;
   HIP_TRY(hipGetLastError());
   L->last_T = T;
@@ -276,6 +303,12 @@ int hy3x_layer_stats(hy3x_layer *L, uint64_t *forwards, uint64_t *experts_touche
   if (forwards) *forwards = h[0];
   if (experts_touched) *experts_touched = h[1];
   if (reset) HIP_TRY(hipMemset(L->stats, 0, sizeof(h)));
+  return HY3X_OK;
+}
+
+int hy3x_layer_set_trace(hy3x_layer *L, int stage, void *buf) {
+  if (!L || stage < 0 || stage > 2) return fail(HY3X_E_ARG, "bad argument");
+  L->trace[stage] = (unsigned long long *)buf;
   return HY3X_OK;
 }
 

@@ -55,16 +55,25 @@ __device__ __forceinline__ BlockScale block_scale(const uint4 &hdr, const ScaleS
   return r;
 }
 
+// (a & m) | o in one VALU op (v_and_or_b32); the compiler otherwise often
+// emits an AND and an OR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+  return r;
+}
+
 // fp16 pairs of the 64 nibbles of one group: P[4j+0..3] pair with X[4j+0..3].
 __device__ __forceinline__ void unpack_group(const uint4 &q0, const uint4 &q1, uint32_t (&P)[32]) {
   const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  const uint32_t mag = 0x64006400u;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const uint32_t a = w[j], b = a >> 8;
-    P[4 * j + 0] = (a & 0x000F000Fu) | 0x64006400u;
-    P[4 * j + 1] = (a & 0x00F000F0u) | 0x64006400u;
-    P[4 * j + 2] = (b & 0x000F000Fu) | 0x64006400u;
-    P[4 * j + 3] = (b & 0x00F000F0u) | 0x64006400u;
+    P[4 * j + 0] = and_or(a, 0x000F000Fu, mag);
+    P[4 * j + 1] = and_or(a, 0x00F000F0u, mag);
+    P[4 * j + 2] = and_or(b, 0x000F000Fu, mag);
+    P[4 * j + 3] = and_or(b, 0x00F000F0u, mag);
   }
 }
 

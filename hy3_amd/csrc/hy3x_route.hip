@@ -20,129 +20,45 @@
 // fp32 division and sqrt are correctly rounded (built with
 // -fhip-fp32-correctly-rounded-divide-sqrt) and nothing in this file is
 // contracted into FMAs beyond the explicit fmaf calls.
-#include "hy3x_common.h"
+#include "hy3x_route.h"
 
 #pragma clang fp contract(off)
 
 namespace hy3x {
 
-__device__ __forceinline__ float sig_expf(float xf) {
-  if (xf != xf) return xf;
-  if (xf > 88.72f) return __builtin_huge_valf();
-  if (xf < -87.0f) return 0.0f;
-  const double x = (double)xf;
-  const double kd = __builtin_rint(x * 1.4426950408889634);
-  double r = __builtin_fma(kd, -6.93147180369123816490e-01, x);
-  r = __builtin_fma(kd, -1.90821492927058770002e-10, r);
-  double p = 1.0 / 6227020800.0;
-  p = __builtin_fma(p, r, 1.0 / 479001600.0);
-  p = __builtin_fma(p, r, 1.0 / 39916800.0);
-  p = __builtin_fma(p, r, 1.0 / 3628800.0);
-  p = __builtin_fma(p, r, 1.0 / 362880.0);
-  p = __builtin_fma(p, r, 1.0 / 40320.0);
-  p = __builtin_fma(p, r, 1.0 / 5040.0);
-  p = __builtin_fma(p, r, 1.0 / 720.0);
-  p = __builtin_fma(p, r, 1.0 / 120.0);
-  p = __builtin_fma(p, r, 1.0 / 24.0);
-  p = __builtin_fma(p, r, 1.0 / 6.0);
-  p = __builtin_fma(p, r, 0.5);
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
-  const long long k = (long long)kd;
-  const double sc = __longlong_as_double((long long)((unsigned long long)(k + 1023) << 52));
-  return (float)(p * sc);
-}
+// Chain-transposed LDS rows: buf[v*RS + i] = a[8i+v]. RS = 512 + 4 keeps the
+// eight chains' float4 reads on distinct banks.
+constexpr int NI = D / 8;  // 512 steps per chain
+constexpr int RS = NI + 4;
 
-__device__ __forceinline__ float sigmoid_c(float l) { return 1.0f / (1.0f + sig_expf(-l)); }
-
-// ((c1+c5)+(c3+c7)) + ((c0+c4)+(c2+c6))
-__device__ __forceinline__ float tree8(const float (&c)[8]) {
-  const float t0 = c[0] + c[4], t1 = c[1] + c[5], t2 = c[2] + c[6], t3 = c[3] + c[7];
-  const float u0 = t2 + t0, u1 = t3 + t1;
-  return u1 + u0;
-}
-
-// Same tree over 8 consecutive lanes (lane group g8 = lane & ~7 holds c[0..7]);
-// every lane of the group gets the result.
-__device__ __forceinline__ float tree8_lanes(float c, int v) {
-  const float c4 = __shfl_xor(c, 4, 64);           // lanes v<4: c[v+4]
-  const float t = c + c4;                            // t_v = c_v + c_{v+4} (v<4)
-  const float t2 = __shfl_xor(t, 2, 64);           // v=0: t2 ; v=1: t3
-  const float u = t2 + t;                            // u0 = t2+t0 (v=0), u1 = t3+t1 (v=1)
-  const float u1 = __shfl_xor(u, 1, 64);           // v=0 gets u1
-  const float res = u1 + u;                          // v=0: u1 + u0
-  return __shfl(res, (threadIdx.x & 63) & ~7, 64);
-}
-
-// Parallel selection-with-swaps top-K over 192 scores held 3 per lane
-// (expert e at lane e%64, slot e/64). Lane 0 writes ids[0..K).
-__device__ void wave_topk(const float (&sc)[3], int lane, int K, int32_t *ids) {
-  int pos[3] = {lane, lane + 64, lane + 128};
-  bool sel[3] = {false, false, false};
-  for (int k = 0; k < K; k++) {
-    float bv = -__builtin_huge_valf();
-    int bp = 0x7fffffff, be = -1;
-#pragma unroll
-    for (int m = 0; m < 3; m++) {
-      if (!sel[m] && (sc[m] > bv || (sc[m] == bv && pos[m] < bp))) {
-        bv = sc[m];
-        bp = pos[m];
-        be = lane + 64 * m;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int op = __shfl_xor(bp, o, 64), oe = __shfl_xor(be, o, 64);
-      if (ov > bv || (ov == bv && op < bp)) {
-        bv = ov;
-        bp = op;
-        be = oe;
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 3; m++) {
-      if (!sel[m] && pos[m] == k) pos[m] = bp;  // the element at position k moves
-      if (lane + 64 * m == be) {
-        sel[m] = true;
-        pos[m] = k;
-      }
-    }
-    if (lane == 0) ids[k] = be;
+__device__ __forceinline__ void load_transposed(const float *src, float *buf, int lane,
+                                                int nthreads) {
+  const float4 *g = reinterpret_cast<const float4 *>(src);
+#pragma unroll 4
+  for (int q = lane; q < D / 4; q += nthreads) {
+    const float4 a = g[q];
+    const int j = 4 * q, v = j & 7, i = j >> 3;  // j..j+3 share i; v = 0 or 4
+    buf[(v + 0) * RS + i] = a.x;
+    buf[(v + 1) * RS + i] = a.y;
+    buf[(v + 2) * RS + i] = a.z;
+    buf[(v + 3) * RS + i] = a.w;
   }
 }
 
-// sigmoid, biased scores, top-K and weights of one token by one wave.
-__device__ void route_from_logits(const float *lg, const float *bias, int has_bias, int K,
-                                  float scale, int32_t *ids, float *wpre, float *wout,
-                                  float *sg_l, int32_t *sel_ids) {
-  const int lane = threadIdx.x & 63;
-  float sc[3];
-#pragma unroll
-  for (int m = 0; m < 3; m++) {
-    const int e = lane + 64 * m;
-    const float sgm = sigmoid_c(lg[e]);
-    sg_l[e] = sgm;
-    sc[m] = has_bias ? sgm + bias[e] : sgm;
+// One fmaf chain over a chain-transposed row pair (512 steps).
+__device__ __forceinline__ float chain_dot(const float *a, const float *b) {
+  const float4 *av = reinterpret_cast<const float4 *>(a);
+  const float4 *bv = reinterpret_cast<const float4 *>(b);
+  float acc = 0.0f;
+#pragma unroll 16
+  for (int q = 0; q < NI / 4; q++) {
+    const float4 x = av[q], y = bv[q];
+    acc = __builtin_fmaf(x.x, y.x, acc);
+    acc = __builtin_fmaf(x.y, y.y, acc);
+    acc = __builtin_fmaf(x.z, y.z, acc);
+    acc = __builtin_fmaf(x.w, y.w, acc);
   }
-  wave_topk(sc, lane, K, sel_ids);
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  if (lane == 0) {
-    float sum = 0.0f;
-    for (int k = 0; k < K; k++) sum += sg_l[sel_ids[k]];
-    const float inv = 1.0f / (sum + 1e-20f);
-    for (int k = 0; k < K; k++) {
-      const float v = sg_l[sel_ids[k]] * inv;
-      ids[k] = sel_ids[k];
-      wpre[k] = v;
-      wout[k] = v * scale;
-    }
-  }
-}
-
-__device__ __forceinline__ void stage_store(__half *dst, int j, float v) {
-  dst[stage_index(j)] = __float2half(v);
+  return acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -152,134 +68,89 @@ __device__ __forceinline__ void stage_store(__half *dst, int j, float v) {
 // the eight logit chains. The last block of a token (atomic ticket) runs the
 // top-K and resets the ticket, so the kernel can be relaunched or replayed
 // without clearing memory. Block (0, t) also stages s for the expert kernels.
-__global__ __launch_bounds__(64) void k_router_small(
+__global__ __launch_bounds__(256) void k_router_logits(
     const float *__restrict__ x, const float *__restrict__ norm_w,
-    const float *__restrict__ router, const float *__restrict__ bias, int has_bias, int K,
-    float scale, float *logits, __half *__restrict__ s16, float *__restrict__ s32,
-    int32_t *__restrict__ ids, float *__restrict__ wpre, float *__restrict__ wout,
-    unsigned *__restrict__ tickets) {
-  constexpr int NI = D / 8;  // 512 steps per chain
-  __shared__ float4 xs[8][NI / 4], ws[8][NI / 4], rs[8][NI / 4];
-  const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)t * D);
-  const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
-  const float4 *rg = reinterpret_cast<const float4 *>(router + (size_t)e * D);
-  float *xsf = &xs[0][0].x, *wsf = &ws[0][0].x, *rsf = &rs[0][0].x;
-#pragma unroll 4
-  for (int q = lane; q < D / 4; q += 64) {
-    const float4 a = xg[q], b = wg[q], c = rg[q];
-    const int j = 4 * q, v = j & 7, i = j >> 3;  // j..j+3 share i; v = 0 or 4
-    xsf[(v + 0) * NI + i] = a.x; xsf[(v + 1) * NI + i] = a.y;
-    xsf[(v + 2) * NI + i] = a.z; xsf[(v + 3) * NI + i] = a.w;
-    wsf[(v + 0) * NI + i] = b.x; wsf[(v + 1) * NI + i] = b.y;
-    wsf[(v + 2) * NI + i] = b.z; wsf[(v + 3) * NI + i] = b.w;
-    rsf[(v + 0) * NI + i] = c.x; rsf[(v + 1) * NI + i] = c.y;
-    rsf[(v + 2) * NI + i] = c.z; rsf[(v + 3) * NI + i] = c.w;
-  }
-  __syncthreads();
-  __shared__ float r_sh;
-  if (lane < 8) {  // sum-of-squares chain `lane`
-    float acc = 0.0f;
-    const float4 *xv = xs[lane];
-#pragma unroll 8
-    for (int q = 0; q < NI / 4; q++) {
-      const float4 a = xv[q];
-      acc = __builtin_fmaf(a.x, a.x, acc);
-      acc = __builtin_fmaf(a.y, a.y, acc);
-      acc = __builtin_fmaf(a.z, a.z, acc);
-      acc = __builtin_fmaf(a.w, a.w, acc);
+    const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
+    float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
+    __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace) {
+  __shared__ __attribute__((aligned(16))) float xsf[8 * RS], wsf[8 * RS], rsf[8 * RS];
+  const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  trace_point(trace, 0);
+  float r_blk;
+  {  // every load in flight at once: 4 float4 of each row per thread
+    const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)t * D);
+    const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
+    const float4 *rg = reinterpret_cast<const float4 *>(router + (size_t)e * D);
+    float4 a[4], b[4], c[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      a[u] = xg[tid + 256 * u];
+      b[u] = wg[tid + 256 * u];
+      c[u] = rg[tid + 256 * u];
     }
-    const float ss = tree8_lanes(acc, lane);
-    if (lane == 0) r_sh = 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int j = 4 * (tid + 256 * u), v = j & 7, i = j >> 3;
+      xsf[(v + 0) * RS + i] = a[u].x; xsf[(v + 1) * RS + i] = a[u].y;
+      xsf[(v + 2) * RS + i] = a[u].z; xsf[(v + 3) * RS + i] = a[u].w;
+      wsf[(v + 0) * RS + i] = b[u].x; wsf[(v + 1) * RS + i] = b[u].y;
+      wsf[(v + 2) * RS + i] = b[u].z; wsf[(v + 3) * RS + i] = b[u].w;
+      rsf[(v + 0) * RS + i] = c[u].x; rsf[(v + 1) * RS + i] = c[u].y;
+      rsf[(v + 2) * RS + i] = c[u].z; rsf[(v + 3) * RS + i] = c[u].w;
+    }
+    __shared__ float red_l[4];
+    const float ss = block_sumsq(a, red_l);  // contains the barrier for the LDS rows
+    r_blk = 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
   }
+  trace_point(trace, 1);
+  const float r = r_blk;
+  for (int q = tid; q < 8 * RS; q += 256) xsf[q] = (xsf[q] * wsf[q]) * r;  // s, in place
   __syncthreads();
-  const float r = r_sh;
-  // s = (x*w)*r, in place over xs (chain-transposed)
-  for (int q = lane; q < D; q += 64) xsf[q] = (xsf[q] * wsf[q]) * r;
-  __syncthreads();
-  if (e == 0) {  // stage s for the expert kernels (fp16 pair-staged and fp32)
-    for (int j = lane; j < D; j += 64) {
-      const float sv = xsf[(j & 7) * NI + (j >> 3)];
+  if (tid < 8) {  // logit chain `tid`
+    const float lg = tree8_lanes(chain_dot(rsf + tid * RS, xsf + tid * RS), tid);
+    if (tid == 0) {
+      const float sg = sigmoid_c(lg);
+      logits[(size_t)t * E + e] = lg;
+      sig[(size_t)t * E + e] = sg;
+      score[(size_t)t * E + e] = has_bias ? sg + bias[e] : sg;
+    }
+    trace_point(trace, 3);
+  } else if (e == 0) {  // stage s for the expert kernels (fp16 pair-staged and fp32)
+    for (int j = tid - 8; j < D; j += 248) {
+      const float sv = xsf[(j & 7) * RS + (j >> 3)];
       stage_store(s16 + (size_t)t * D, j, sv);
       s32[(size_t)t * D + j] = sv;
     }
   }
-  if (lane < 8) {  // logit chain `lane`
-    float acc = 0.0f;
-    const float4 *sv = xs[lane], *rv = rs[lane];
-#pragma unroll 8
-    for (int q = 0; q < NI / 4; q++) {
-      const float4 a = rv[q], b = sv[q];
-      acc = __builtin_fmaf(a.x, b.x, acc);
-      acc = __builtin_fmaf(a.y, b.y, acc);
-      acc = __builtin_fmaf(a.z, b.z, acc);
-      acc = __builtin_fmaf(a.w, b.w, acc);
-    }
-    const float lg = tree8_lanes(acc, lane);
-    if (lane == 0) {
-      logits[(size_t)t * E + e] = lg;
-      __threadfence();
-    }
-  }
-  __shared__ int is_last;
-  if (lane == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&tickets[t], 1u, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __atomic_thread_fence(__ATOMIC_ACQUIRE);
-  __shared__ float sg_l[E], lg_l[E];
-  __shared__ int32_t sel_ids[KMAX];
-  for (int ee = lane; ee < E; ee += 64) lg_l[ee] = logits[(size_t)t * E + ee];
-  __syncthreads();
-  route_from_logits(lg_l, bias, has_bias, K, scale, ids + (size_t)t * K, wpre + (size_t)t * K,
-                    wout + (size_t)t * K, sg_l, sel_ids);
-  if (lane == 0) tickets[t] = 0u;
 }
 
 // ---------------------------------------------------------------------------
 // Large T: (1) RMSNorm per token, one wave per token (chains over LDS);
 // (2) router GEMM, LDS-tiled SIMT, each output keeping its eight chains;
 // (3) top-K, one wave per token.
-__global__ __launch_bounds__(64) void k_rmsnorm(const float *__restrict__ x,
-                                                const float *__restrict__ norm_w,
-                                                __half *__restrict__ s16,
-                                                float *__restrict__ s32) {
-  constexpr int NI = D / 8;
-  __shared__ float4 xs[8][NI / 4];
-  const int t = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
+                                                 const float *__restrict__ norm_w,
+                                                 __half *__restrict__ s16,
+                                                 float *__restrict__ s32) {
+  const int t = blockIdx.x, tid = threadIdx.x;
   const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)t * D);
-  float *xsf = &xs[0][0].x;
-  for (int q = lane; q < D / 4; q += 64) {
-    const float4 a = xg[q];
-    const int j = 4 * q, v = j & 7, i = j >> 3;
-    xsf[(v + 0) * NI + i] = a.x; xsf[(v + 1) * NI + i] = a.y;
-    xsf[(v + 2) * NI + i] = a.z; xsf[(v + 3) * NI + i] = a.w;
-  }
-  __syncthreads();
-  __shared__ float r_sh;
-  if (lane < 8) {
-    float acc = 0.0f;
-    const float4 *xv = xs[lane];
-#pragma unroll 8
-    for (int q = 0; q < NI / 4; q++) {
-      const float4 a = xv[q];
-      acc = __builtin_fmaf(a.x, a.x, acc);
-      acc = __builtin_fmaf(a.y, a.y, acc);
-      acc = __builtin_fmaf(a.z, a.z, acc);
-      acc = __builtin_fmaf(a.w, a.w, acc);
-    }
-    const float ss = tree8_lanes(acc, lane);
-    if (lane == 0) r_sh = 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
-  }
-  __syncthreads();
-  const float r = r_sh;
-  for (int j = lane; j < D; j += 64) {
-    const float sv = (x[(size_t)t * D + j] * norm_w[j]) * r;
-    s32[(size_t)t * D + j] = sv;
-    stage_store(s16 + (size_t)t * D, j, sv);
+  const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
+  float4 a[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) a[u] = xg[tid + 256 * u];
+  __shared__ float red_l[4];
+  const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const float4 w = wg[tid + 256 * u];
+    const int j = 4 * (tid + 256 * u);
+    const float4 sv = make_float4((a[u].x * w.x) * r, (a[u].y * w.y) * r, (a[u].z * w.z) * r,
+                                  (a[u].w * w.w) * r);
+    reinterpret_cast<float4 *>(s32 + (size_t)t * D)[tid + 256 * u] = sv;
+    stage_store(s16 + (size_t)t * D, j + 0, sv.x);
+    stage_store(s16 + (size_t)t * D, j + 1, sv.y);
+    stage_store(s16 + (size_t)t * D, j + 2, sv.z);
+    stage_store(s16 + (size_t)t * D, j + 3, sv.w);
   }
 }
 
@@ -350,71 +221,86 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
     }
 }
 
-__global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits,
-                                             const float *__restrict__ bias, int has_bias, int K,
-                                             float scale, int32_t *__restrict__ ids,
-                                             float *__restrict__ wpre, float *__restrict__ wout) {
+// Routing of one token per block (large-T path): sigmoid and scores of the
+// 192 logits, then the top-K.
+__global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
+                                              const float *__restrict__ bias, int has_bias, int K,
+                                              float scale, int32_t *__restrict__ ids,
+                                              float *__restrict__ wpre, float *__restrict__ wout) {
   const int t = blockIdx.x;
-  __shared__ float sg_l[E], lg_l[E];
-  __shared__ int32_t sel_ids[KMAX];
-  for (int e = threadIdx.x; e < E; e += 64) lg_l[e] = logits[(size_t)t * E + e];
+  __shared__ __attribute__((aligned(16))) float sg[E], sc[E], sc_l[E], sg_l[E];
+  __shared__ int32_t scratch_l[4 * E + 2 * KMAX + 2];
+  for (int e = threadIdx.x; e < E; e += 256) {
+    const float v = sigmoid_c(logits[(size_t)t * E + e]);
+    sg[e] = v;
+    sc[e] = has_bias ? v + bias[e] : v;
+  }
   __syncthreads();
-  route_from_logits(lg_l, bias, has_bias, K, scale, ids + (size_t)t * K, wpre + (size_t)t * K,
-                    wout + (size_t)t * K, sg_l, sel_ids);
+  topk_block(sg, sc, K, scale, ids + (size_t)t * K, wpre + (size_t)t * K, wout + (size_t)t * K,
+             sc_l, sg_l, scratch_l);
 }
 
-// Device dispatch: per-expert slot lists and the work-tile list, one block.
+// Device dispatch: per-expert slot lists and the work-tile list, one block of
+// 256 threads (four waves; expert e is handled by thread e).
 // Slots: s < T*K is (token s/K, rank s%K) of a routed expert; s = T*K + t is
 // token t of the shared expert (index E), which every token uses.
 // tiles[i] = {expert, first list index, count <= NT, 0}.
-__global__ __launch_bounds__(1024) void k_dispatch(const int32_t *__restrict__ ids, int T, int K,
-                                                   int NT, int32_t *__restrict__ list,
-                                                   int4 *__restrict__ tiles,
-                                                   int32_t *__restrict__ n_tiles, int max_tiles,
-                                                   int32_t *__restrict__ counts_out,
-                                                   unsigned long long *__restrict__ stats) {
-  __shared__ int cnt[E + 1], off[E + 2], cur[E + 1], toff[E + 2];
-  const int tid = threadIdx.x, n = T * K;
-  for (int e = tid; e <= E; e += blockDim.x) {
-    cnt[e] = 0;
-    cur[e] = 0;
+__device__ __forceinline__ int block_exclusive_scan256(int v, int *tmp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
   }
+  if (lane == 63) tmp[wave] = incl;
   __syncthreads();
-  for (int i = tid; i < n; i += blockDim.x) {
+  int base = 0;
+  for (int w = 0; w < wave; w++) base += tmp[w];
+  __syncthreads();
+  return base + incl - v;
+}
+
+__global__ __launch_bounds__(256) void k_dispatch(const int32_t *__restrict__ ids, int T, int K,
+                                                  int NT, int32_t *__restrict__ list,
+                                                  int4 *__restrict__ tiles,
+                                                  int32_t *__restrict__ n_tiles, int max_tiles,
+                                                  int32_t *__restrict__ counts_out,
+                                                  unsigned long long *__restrict__ stats) {
+  __shared__ int cnt[256], cur[256], tmp[8];
+  const int tid = threadIdx.x, n = T * K;
+  cnt[tid] = 0;
+  cur[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += 256) {
     const int e = ids[i];
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
-  if (tid == 0) cnt[E] = T;
   __syncthreads();
-  if (tid == 0) {
-    int a = 0, b = 0;
-    for (int e = 0; e <= E; e++) {
-      off[e] = a;
-      toff[e] = b;
-      a += cnt[e];
-      b += (cnt[e] + NT - 1) / NT;
-    }
-    off[E + 1] = a;
-    toff[E + 1] = b;
-    *n_tiles = b < max_tiles ? b : max_tiles;
+  const int c = tid < E ? cnt[tid] : (tid == E ? T : 0);
+  const int off = block_exclusive_scan256(c, tmp);
+  const int nt = (c + NT - 1) / NT;
+  const int toff = block_exclusive_scan256(nt, tmp);
+  const int active = block_exclusive_scan256(c > 0 ? 1 : 0, tmp);
+  if (tid == 255) {
+    *n_tiles = toff < max_tiles ? toff : max_tiles;
     if (stats) {  // forwards, experts touched (shared included)
-      int active = 0;
-      for (int e = 0; e <= E; e++) active += cnt[e] > 0;
       stats[0] += 1ull;
       stats[1] += (unsigned long long)active;
     }
   }
+  __shared__ int offs[256];
+  offs[tid] = off;
   __syncthreads();
-  for (int i = tid; i < n; i += blockDim.x) {
+  for (int i = tid; i < n; i += 256) {
     const int e = ids[i];
-    if (e >= 0 && e < E) list[off[e] + atomicAdd(&cur[e], 1)] = i;
+    if (e >= 0 && e < E) list[offs[e] + atomicAdd(&cur[e], 1)] = i;
   }
-  for (int t = tid; t < T; t += blockDim.x) list[off[E] + t] = n + t;
-  for (int e = tid; e <= E; e += blockDim.x) {
-    if (counts_out) counts_out[e] = cnt[e];
-    const int c = cnt[e];
-    for (int j = 0, ti = toff[e]; j * NT < c && ti < max_tiles; j++, ti++)
-      tiles[ti] = make_int4(e, off[e] + j * NT, min(NT, c - j * NT), 0);
+  for (int t = tid; t < T; t += 256) list[offs[E] + t] = n + t;
+  if (tid <= E) {
+    if (counts_out) counts_out[tid] = c;
+    for (int j = 0, ti = toff; j * NT < c && ti < max_tiles; j++, ti++)
+      tiles[ti] = make_int4(tid, off + j * NT, min(NT, c - j * NT), 0);
   }
 }
 

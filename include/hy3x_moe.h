@@ -118,6 +118,11 @@ int hy3x_layer_stage_times(hy3x_layer *layer, float *ms, int n_stages, int *n_fo
 int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_touched,
                      int reset);
 
+/* Diagnostics: per-block timestamps of the decode kernels (stage 0 router,
+ * 1 gate/up, 2 down). buf: device memory of 8 x 64-bit words per block, or
+ * NULL to stop. Each block writes REALTIME-counter (100 MHz) checkpoints. */
+int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
+
 /* Execution-path override for tests: 0 = automatic (by T), 1 = force the
  * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path. */
 int hy3x_layer_set_path(hy3x_layer *layer, int path);

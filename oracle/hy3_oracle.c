@@ -298,12 +298,43 @@ float hy3o_sig_expf(float xf) {
   return (float)(p * s);
 }
 
-/* RMSNorm (hy3.c:435-444) as built: ss in the 8-chain order, r = 1/sqrt(ss/n
- * + eps) correctly rounded (the build uses an rsqrt estimate refined by one
- * Newton step, whose last bit depends on the host CPU), out = (x * w) * r (the
- * build's reassociation of x * r * w). */
+/* RMSNorm (hy3.c:435-444) with n = 4096: ss in the block order above, r =
+ * 1/sqrt(ss/n + eps) correctly rounded (the build uses an rsqrt estimate
+ * refined by one Newton step, whose last bits depend on the host CPU), out =
+ * (x * w) * r (the build's reassociation of x * r * w). */
+/* Sum of squares over 4096 elements in the order of a 256-thread block:
+ * thread t accumulates x[1024i + 4t + c]^2 with fmaf for i = 0..3 (outer),
+ * c = 0..3 (inner) from 0; each 64-thread wave reduces with v[l] += v[l^1],
+ * v[l] += v[l^2], v[l] += v[mirror8(l)], v[l] += v[mirror16(l)], its total is
+ * (v[0] + v[16]) + (v[32] + v[48]); the block total is (W0 + W1) + (W2 + W3).
+ * (The reference build's r comes from an rsqrt estimate whose bits depend on
+ * the host CPU, so no summation order reproduces it; this one is fast on the
+ * GPU and restated exactly here.) */
+float hy3o_sumsq_block(const float *x) {
+  float W[4];
+  for (int w = 0; w < 4; w++) {
+    float v[64], u[64];
+    for (int l = 0; l < 64; l++) {
+      const int t = 64 * w + l;
+      float acc = 0.0f;
+      for (int i = 0; i < 4; i++)
+        for (int c = 0; c < 4; c++) {
+          const float a = x[1024 * i + 4 * t + c];
+          acc = fmaf(a, a, acc);
+        }
+      v[l] = acc;
+    }
+    for (int l = 0; l < 64; l++) u[l] = v[l] + v[l ^ 1];
+    for (int l = 0; l < 64; l++) v[l] = u[l] + u[l ^ 2];
+    for (int l = 0; l < 64; l++) u[l] = v[l] + v[(l & ~7) | (7 - (l & 7))];
+    for (int l = 0; l < 64; l++) v[l] = u[l] + u[(l & ~15) | (15 - (l & 15))];
+    W[w] = (v[0] + v[16]) + (v[32] + v[48]);
+  }
+  return (W[0] + W[1]) + (W[2] + W[3]);
+}
+
 static float rms_scale(const float *x, int n) {
-  const float ss = hy3o_dot8(x, x, n);
+  const float ss = hy3o_sumsq_block(x);
   return 1.0f / sqrtf(ss / (float)n + HY3O_RMS_EPS);
 }
 

@@ -73,6 +73,8 @@ void hy3o_gen_q4k_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float s
  * j = 8i+v, then ((a1+a5)+(a3+a7)) + ((a0+a4)+(a2+a6)). */
 float hy3o_dot8(const float *a, const float *b, int n);
 float hy3o_sig_expf(float x);                 /* exp for the router sigmoid */
+/* Sum of squares of 4096 values in the GPU block's fixed order. */
+float hy3o_sumsq_block(const float *x);                 /* exp for the router sigmoid */
 void hy3o_rms_norm(float *out, const float *x, const float *w, int n);
 /* Full routing for one token: s (normalised input) is written to s_out if
  * non-NULL; logits/sigmoid/score (E each) if non-NULL; ids[K], wpre[K] (before

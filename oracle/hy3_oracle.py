@@ -39,6 +39,7 @@ _SIGS = {
     "hy3o_gen_q4k_matrix": (None, [P, I32, I32, U64, F32]),
     "hy3o_dot8": (F32, [P, P, I32]),
     "hy3o_sig_expf": (F32, [F32]),
+    "hy3o_sumsq_block": (F32, [P]),
     "hy3o_rms_norm": (None, [P, P, P, I32]),
     "hy3o_route_token": (None, [P, P, P, P, I32, I32, F32, P, P, P, P, P, P, P]),
     "hy3o_route_token_r": (None, [P, P, P, P, I32, I32, F32, F32, P, P, P, P, P, P, P]),

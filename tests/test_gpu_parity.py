@@ -250,3 +250,49 @@ def test_stack_routing_per_layer(torch):
         assert O.rel_l2(xc, yc) <= TOL
     for L in layers:
         L.close()
+
+
+@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("case", ["all_equal", "bias_ties", "some_ties"])
+def test_routing_with_ties(torch, T, case):
+    """Tied scores: the selection-with-swaps order (hy3.c:654-666) decides, on
+    both router paths (decode T=1 and the large-T path)."""
+    L = H.MoELayer(16)
+    L.synth_experts(C.WEIGHT_SEED, 0)
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    if case == "all_equal":
+        rt = np.zeros_like(rt)
+        b = np.zeros_like(b)
+    elif case == "bias_ties":
+        rt = np.zeros_like(rt)
+        b = (np.arange(E) % 5).astype(np.float32) * 0.25
+    else:
+        b = b.copy()
+        b[[3, 77, 150]] = 50.0  # three tied winners with identical huge bias
+        b[[10, 11]] = 40.0
+    L.set_router(nw, rt, b)
+    cpu = O.SynthLayer(C.WEIGHT_SEED)
+    cpu.router, cpu.bias = np.ascontiguousarray(rt.ravel()), b
+    x = C.inputs(0xC1, T)
+    _, ids, wpre, _ = run(torch, L, x)
+    L.close()
+    r = cpu.route(x)
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 7, 64, 200])
+def test_expert_paths_match_oracle(torch, layer, cpu, T):
+    """Every expert path (0 automatic, 1 wavefront GEMV, 2 MFMA grouped GEMM)
+    meets the tolerance on the same tokens; routing is identical on all."""
+    x = C.inputs(0xC2, T, first_token=300)
+    rows = np.linspace(0, T - 1, min(T, 6)).astype(int)
+    yo, ro = cpu.forward(x[rows])
+    try:
+        for path in (0, 1, 2):
+            layer.set_path(path)
+            y, ids, _, _ = run(torch, layer, x)
+            assert np.array_equal(ids[rows], ro["ids"]), path
+            assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL, path
+    finally:
+        layer.set_path(0)
