@@ -42,7 +42,7 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
                                                const int4 *, const int32_t *, float *);
 
 template <bool GATEUP>
-__global__ void k_moe_mfma(const uint8_t *wq, const __half *act, const int32_t *list,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(const uint8_t *wq, const __half *act, const int32_t *list,
                            const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m,
                            float *out);
 extern template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const int32_t *,

@@ -40,17 +40,17 @@ __device__ __forceinline__ uint32_t h2_splat(float v) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Per-lane dequantisation state of one Q4_K block of one row: fp16 pairs of
-// (d*sc_j) and -(dmin*m_j) for the 8 sub-blocks (odd j carry d*sc/16 because
-// the high-nibble unpack yields 16q).
-struct BlockF16 {
-  uint32_t sc2[8], mn2[8];
+// Per-lane state of one Q4_K block of one row: fp16 pairs (sc_j, sc_j) and
+// (-1024 sc_j, -1024 sc_j) for the 8 sub-blocks, and the 6-bit mins. All
+// exact in fp16.
+struct BlockI16 {
+  uint32_t sc2[8], nb2[8];
+  uint32_t m[8];
 };
 
-__device__ __forceinline__ BlockF16 block_f16(const uint4 &hdr) {
-  const float d = fp16_quirk(hdr.x & 0xffffu), dmin = fp16_quirk(hdr.x >> 16);
+__device__ __forceinline__ BlockI16 block_i16(const uint4 &hdr) {
   const uint32_t s03 = hdr.y, s47 = hdr.z, s811 = hdr.w;
-  BlockF16 r;
+  BlockI16 r;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     uint32_t sc, m;
@@ -61,33 +61,42 @@ __device__ __forceinline__ BlockF16 block_f16(const uint4 &hdr) {
       sc = bfe(s811, 8 * (j - 4), 4) | (bfe(s03, 8 * (j - 4) + 6, 2) << 4);
       m = bfe(s811, 8 * (j - 4) + 4, 4) | (bfe(s47, 8 * (j - 4) + 6, 2) << 4);
     }
-    const float a = d * (float)sc * ((j & 1) ? 0.0625f : 1.0f);
-    r.sc2[j] = h2_splat(a);
-    r.mn2[j] = h2_splat(-(dmin * (float)m));
+    r.sc2[j] = h2_splat((float)sc);
+    r.nb2[j] = h2_splat(-1024.0f * (float)sc);
+    r.m[j] = m;
   }
   return r;
 }
 
-// A operand (8 fp16 = 4 dwords) for sub-block 2p (hi = false) or 2p+1 (hi =
-// true) from the 8 bytes qs[32p + 8g .. +7] of this lane's row.
-__device__ __forceinline__ h8_t dequant_a(uint2 q, bool hi, uint32_t sc2, uint32_t mn2) {
-  const uint32_t mag = 0x64006400u, m1024 = 0xE400E400u;  // fp16 pair (-1024, -1024)
-  const uint32_t mask = hi ? 0x00F000F0u : 0x000F000Fu;
+// A operand for sub-block 2p (hi = false) or 2p+1 (hi = true): the exact
+// integers sc*q in fp16 (sc*q <= 945), from the 8 bytes qs[32p + 8g .. +7].
+// (1024 + q)*sc - 1024*sc is computed by one fused multiply-add whose exact
+// result is representable, so it is exact.
+__device__ __forceinline__ h8_t dequant_a(uint2 q, bool hi, uint32_t sc2, uint32_t nb2) {
+  const uint32_t mag = 0x64006400u, mask = 0x000F000Fu;
+  const int sh = hi ? 4 : 0;
   uint32_t p[4];
-  p[0] = and_or(q.x, mask, mag);
-  p[1] = and_or(q.x >> 8, mask, mag);
-  p[2] = and_or(q.y, mask, mag);
-  p[3] = and_or(q.y >> 8, mask, mag);
+  p[0] = and_or(q.x >> sh, mask, mag);
+  p[1] = and_or(q.x >> (8 + sh), mask, mag);
+  p[2] = and_or(q.y >> sh, mask, mag);
+  p[3] = and_or(q.y >> (8 + sh), mask, mag);
 #pragma unroll
-  for (int i = 0; i < 4; i++) p[i] = pk_fma_f16(pk_add_f16(p[i], m1024), sc2, mn2);
+  for (int i = 0; i < 4; i++) p[i] = pk_fma_f16(p[i], sc2, nb2);
   return __builtin_bit_cast(h8_t, *reinterpret_cast<uint4 *>(p));
 }
 
 // Grouped GEMM over the tile list. GATEUP: A = gate and up rows of the expert
 // (K = 4096), B = staged s, epilogue h = silu(g) * u -> h16m[slot][perm8(row)]
 // (fp16). Otherwise A = down rows (K = 1536), B = h16m, out[slot][row] fp32.
+//
+// Per block column: Dblk = sum over the 8 sub-blocks of MFMA(sc*q, x) (exact
+// integer weights, fp16 activations, fp32 accumulation), Dmin = MFMA of the
+// 6-bit mins against the tokens' sub-block sums of x (each sum split into two
+// fp16 parts), and acc += d * Dblk - dmin * Dmin with d, dmin of the D rows in
+// fp32 -- the Q4_K identity sum_k w_k x_k = d sum_j sc_j sum_{k in j} q_k x_k
+// - dmin sum_j m_j sum_{k in j} x_k.
 template <bool GATEUP>
-__global__ __launch_bounds__(256) void k_moe_mfma(const uint8_t *__restrict__ wq,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(const uint8_t *__restrict__ wq,
                                                   const __half *__restrict__ act,
                                                   const int32_t *__restrict__ list,
                                                   const int4 *__restrict__ tiles,
@@ -107,6 +116,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(const uint8_t *__restrict__ wq
   const int lr = lane & 15, g = lane >> 4;
 
   __shared__ __attribute__((aligned(16))) _Float16 bt[MT_TOK][BT_STRIDE];
+  __shared__ __attribute__((aligned(16))) _Float16 bm[MT_TOK][16];  // sub-block sums (hi, lo)
   __shared__ int32_t slot_l[MT_TOK], arow_l[MT_TOK];
   if (tid < MT_TOK) {
     const int s = tid < n ? list[o + tid] : -1;
@@ -128,6 +138,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(const uint8_t *__restrict__ wq
   for (int m = 0; m < NMAT; m++)
 #pragma unroll
     for (int t = 0; t < 4; t++) acc[m][t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 
   __syncthreads();
   for (int kb = 0; kb < NKB; kb++) {
@@ -150,22 +161,72 @@ __global__ __launch_bounds__(256) void k_moe_mfma(const uint8_t *__restrict__ wq
       *reinterpret_cast<uint4 *>(&bt[t][8 * c]) = v;
     }
     __syncthreads();
-    BlockF16 bf[NMAT];
+    // sub-block sums of the staged activations, split into two fp16 parts
+    for (int q = tid; q < MT_TOK * 8; q += 256) {
+      const int t = q >> 3, j = q & 7;
+      const h8_t *src = reinterpret_cast<const h8_t *>(&bt[t][32 * j]);
+      const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+      float sum = 0.0f;
 #pragma unroll
-    for (int m = 0; m < NMAT; m++) bf[m] = block_f16(hdr[m]);
+      for (int u = 0; u < 4; u++) {
+        const h8_t v = src[u];
+        sum = __builtin_amdgcn_fdot2((h2_t){v[0], v[1]}, one, sum, false);
+        sum = __builtin_amdgcn_fdot2((h2_t){v[2], v[3]}, one, sum, false);
+        sum = __builtin_amdgcn_fdot2((h2_t){v[4], v[5]}, one, sum, false);
+        sum = __builtin_amdgcn_fdot2((h2_t){v[6], v[7]}, one, sum, false);
+      }
+      const _Float16 hi = (_Float16)sum;
+      const _Float16 lo = (_Float16)(sum - (float)hi);
+      bm[t][2 * j] = hi;
+      bm[t][2 * j + 1] = lo;
+    }
+    __syncthreads();
 #pragma unroll
-    for (int sb = 0; sb < 8; sb++) {
-      h8_t a[NMAT];
+    for (int m = 0; m < NMAT; m++) {
+      const BlockI16 bi = block_i16(hdr[m]);
+      // d, dmin of the D rows 4g + i (row lr of this lane's A is row 4g+i of another lane)
+      const float d_own = fp16_quirk(hdr[m].x & 0xffffu), dm_own = fp16_quirk(hdr[m].x >> 16);
+      float dr[4], dmr[4];
 #pragma unroll
-      for (int m = 0; m < NMAT; m++)
-        a[m] = dequant_a(qv[m][sb >> 1], sb & 1, bf[m].sc2[sb], bf[m].mn2[sb]);
+      for (int i = 0; i < 4; i++) {
+        dr[i] = __shfl(d_own, 4 * g + i, 64);
+        dmr[i] = __shfl(dm_own, 4 * g + i, 64);
+      }
+      // mins operand: k = 2j + h (h: hi/lo part of the sum), k < 16
+      h8_t am;
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const _Float16 mv = g < 2 ? (_Float16)(float)bi.m[4 * g + u] : (_Float16)0.0f;
+        am[2 * u] = mv;
+        am[2 * u + 1] = mv;
+      }
+      f4_t dblk[4];
+#pragma unroll
+      for (int sb = 0; sb < 8; sb++) {
+        const h8_t a = dequant_a(qv[m][sb >> 1], sb & 1, bi.sc2[sb], bi.nb2[sb]);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          if (t < ntt) {
+            const h8_t b = *reinterpret_cast<const h8_t *>(&bt[16 * t + lr][32 * sb + 8 * g]);
+            dblk[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, sb == 0 ? zero4 : dblk[t], 0,
+                                                             0, 0);
+          }
+        }
+      }
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         if (t < ntt) {
-          const h8_t b = *reinterpret_cast<const h8_t *>(&bt[16 * t + lr][32 * sb + 8 * g]);
+          h8_t bmv;
+          if (g < 2) {
+            bmv = *reinterpret_cast<const h8_t *>(&bm[16 * t + lr][8 * g]);
+          } else {
 #pragma unroll
-          for (int m = 0; m < NMAT; m++)
-            acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, acc[m][t], 0, 0, 0);
+            for (int u = 0; u < 8; u++) bmv[u] = (_Float16)0.0f;
+          }
+          const f4_t dmin4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bmv, zero4, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc[m][t][i] = __builtin_fmaf(dr[i], dblk[t][i], __builtin_fmaf(-dmr[i], dmin4[i], acc[m][t][i]));
         }
       }
     }
