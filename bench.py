@@ -10,8 +10,10 @@ token), the configuration of the north-star target; --secondary adds one line
 of results per other configuration inside the same JSON object.
 
 Prints ONE JSON line (rank 0). Fields beyond the driver's contract:
-  roofline      dominant kernel stage: algorithmic bytes per launch / its mean
-                duration from HIP events recorded on the launch stream
+  roofline      dominant kernel: algorithmic bytes per launch / its mean launch
+                duration (HIP events on the launch stream around back-to-back
+                replays of that kernel after the timed steps); traffic = HBM bytes
+                per launch from the committed rocprofv3 PMC summary
   cpu_baseline  the reference CPU MoE block (hy3.c forward_layer_moe built
                 from the reference sources, oracle/_ref) or, when that library
                 is absent, the oracle port, on a bounded token sample
@@ -41,7 +43,36 @@ def parse():
     p.add_argument("--secondary", action="store_true", help="also measure the other configs")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB --steps times (the known-size "
+                        "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload` from the committed rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy-kernel
+    calibration), or None when that kernel/workload has not been counted."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        r = t["workloads"][workload][kernel]
+        return int(r["fetch_bytes"] + r["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_calibration(torch, mib, steps):
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(max(steps, 1)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "launches": max(steps, 1)}))
 
 
 def default_steps(T, n_layers):
@@ -59,6 +90,16 @@ def stage_bytes(stage, U, T, K):
     if stage == "router":
         return 192 * 4096 * 4 + 4096 * 4 + T * 4096 * 4 + T * 4096 * 6
     return 0
+
+
+def dominant_kernel(stage, T, path):
+    """Kernel name of a stage on the path the library picks for T tokens."""
+    if T == 1 and path == 0:
+        return {"gateup": "k_gateup_decode", "down": "k_down_decode"}[stage]
+    mfma = path == 2 or (path == 0 and T >= 64)
+    if mfma:
+        return {"gateup": "k_moe_mfma<true>", "down": "k_moe_mfma<false>"}[stage]
+    return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
 
 
 def measure(torch, H, C, cfg, steps, warmup):
@@ -107,8 +148,13 @@ def measure(torch, H, C, cfg, steps, warmup):
         L.set_timing(False)
     stage_us = {k: v * 1e3 / max(nfw, 1) for k, v in stages.items()}
     dom = max(("gateup", "down"), key=lambda k: stage_us[k])
+    kernel = dominant_kernel(dom, cfg.T, layers[0].path)
     dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K)
-    achieved = dom_bytes / (stage_us[dom] * 1e-6) / 1e9
+    # launch duration of the dominant kernel: replayed back to back on the launch
+    # stream between two HIP events, after the timed forwards
+    reps = max(10, min(steps, 2000))
+    launch_us = layers[-1].time_stage(dom, reps, stream=stream)
+    achieved = dom_bytes / (launch_us * 1e-6) / 1e9
     alg_bytes = C.algorithmic_bytes(cfg.T, U) * cfg.n_layers
     flops = C.algorithmic_flops(cfg.T, cfg.K) * cfg.n_layers
     for L in layers:
@@ -116,9 +162,11 @@ def measure(torch, H, C, cfg, steps, warmup):
     return dict(
         tokens_per_s=tokens_per_s, ms_per_step=ms, U=U, layer_GBps=alg_bytes / (ms * 1e-3) / 1e9,
         layer_TFLOPs=flops / (ms * 1e-3) / 1e12, stage_us=stage_us,
-        roofline=dict(bound="hbm", kernel=dom, achieved=round(achieved, 1), peak=PEAK_HBM_GBS,
-                      unit="GB/s", frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
-                      bytes_per_launch=int(dom_bytes), launch_us=round(stage_us[dom], 3)),
+        roofline=dict(bound="hbm", kernel=kernel, achieved=round(achieved, 1), peak=PEAK_HBM_GBS,
+                      unit="GB/s", frac=round(achieved / PEAK_HBM_GBS, 4),
+                      traffic=measured_traffic(f"config{cfg.index}:{cfg.name}", kernel),
+                      bytes_per_launch=int(dom_bytes), launch_us=round(launch_us, 3),
+                      launch_timing=f"HIP events around {reps} back-to-back launches"),
     )
 
 
@@ -164,6 +212,9 @@ def main():
               "multi-GPU sharding is described in DESIGN.md, not implemented.", file=sys.stderr)
         sys.exit(2)
     import torch
+    if a.copy_calibration:
+        copy_calibration(torch, a.copy_calibration, a.steps)
+        return
     import hy3_amd as H
     from hy3_amd import configs as C
     torch.cuda.init()

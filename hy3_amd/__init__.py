@@ -53,6 +53,7 @@ _SIGS = {
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
+    "hy3x_layer_time_stage": (I32, [P, I32, I32, P, ctypes.POINTER(ctypes.c_float)]),
     "hy3x_layer_set_timing": (I32, [P, I32]),
     "hy3x_layer_set_trace": (I32, [P, I32, P]),
     "hy3x_layer_stats": (I32, [P, ctypes.POINTER(U64), ctypes.POINTER(U64), I32]),
@@ -167,13 +168,24 @@ class MoELayer:
     def synth_experts(self, seed, layer_index=0):
         _check(lib().hy3x_synth_layer_experts(self._h, seed, layer_index))
 
+    path = 0  # 0 auto, 1 GEMV, 2 MFMA (hy3x_layer_set_path)
+
     def set_path(self, path):
         _check(lib().hy3x_layer_set_path(self._h, path))
+        self.path = path
 
     STAGES = ("router", "dispatch", "gateup", "down", "combine")
 
     def set_timing(self, enable):
         _check(lib().hy3x_layer_set_timing(self._h, 1 if enable else 0))
+
+    def time_stage(self, stage, reps, stream=None):
+        """Mean µs per launch of one stage's kernels, replayed `reps` times back to
+        back after the last forward (hy3x_layer_time_stage)."""
+        us = ctypes.c_float()
+        _check(lib().hy3x_layer_time_stage(self._h, self.STAGES.index(stage), reps, stream,
+                                           ctypes.byref(us)))
+        return us.value
 
     def stage_times(self):
         """Accumulated ms per stage since the last reset, and the forward count."""

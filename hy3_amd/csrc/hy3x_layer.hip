@@ -20,6 +20,10 @@
 
 using namespace hy3x;
 
+// Expert path of a forward: single-token fused GEMVs, MFMA grouped GEMM over
+// dispatch tiles, or GEMV over dispatch tiles.
+enum class Mode { DECODE, MFMA, GEMV };
+
 struct hy3x_layer {
   int device = 0;
   int max_tokens = 0;
@@ -35,6 +39,12 @@ struct hy3x_layer {
   unsigned long long *stats = nullptr;
   int max_tiles_alloc = 0;
   int last_T = 0, last_K = 0;
+  struct Forward {  // launch parameters of the current / last forward
+    float *x = nullptr;
+    int T = 0, K = 0, nt = 4, mt = 0;
+    float scale = 1.0f;
+    Mode mode = Mode::GEMV;
+  } cur;
   hipStream_t last_stream = nullptr;
   int path = 0;
   unsigned long long *trace[3] = {nullptr, nullptr, nullptr};
@@ -205,68 +215,114 @@ int hy3x_layer_set_path(hy3x_layer *L, int path) {
   return HY3X_OK;
 }
 
+// Kernels of one stage for the forward described by L->cur (shared by the
+// forward and the kernel replay used for timing).
+static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
+  const auto &c = L->cur;
+  const int T = c.T, K = c.K, mt = c.mt;
+  float *x = c.x;
+  switch (stage) {
+    case HY3X_STAGE_ROUTER:
+      if (T <= kSmallRouterT) {
+        k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias,
+                                                    L->has_bias, L->logits, L->sig, L->score,
+                                                    L->s16, L->s32, L->trace[0]);
+      } else {
+        k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, L->s16, L->s32);
+        k_router_gemm<<<dim3((T + 31) / 32, E / 64), 256, 0, st>>>(L->s32, L->router, T,
+                                                                    L->logits);
+      }
+      if (c.mode != Mode::DECODE)
+        k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, L->ids, L->wpre,
+                                  L->w);
+      break;
+    case HY3X_STAGE_DISPATCH:
+      if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m);
+      if (c.mode != Mode::DECODE)
+        k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, c.nt, L->list, L->tiles, L->n_tiles, mt,
+                                      L->counts, L->stats);
+      break;
+    case HY3X_STAGE_GATEUP:
+      if (c.mode == Mode::DECODE)
+        k_gateup_decode<<<(K + 1) * (F / 32), 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
+                                                            c.scale, L->ids, L->wpre, L->w,
+                                                            L->stats, L->h16, L->trace[1]);
+      else if (c.mode == Mode::MFMA)
+        k_moe_mfma<true><<<mt * (F / 64), 256, 0, st>>>(L->wq, L->s16m, L->list, L->tiles,
+                                                        L->n_tiles, T, K, L->h16m, nullptr);
+      else
+        k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles,
+                                                        L->n_tiles, T, K, L->h16);
+      break;
+    case HY3X_STAGE_DOWN:
+      if (c.mode == Mode::DECODE)
+        k_down_decode<<<D / 16, 576, 0, st>>>(L->wq, L->h16, L->ids, L->w, K, x, L->trace[2]);
+      else if (c.mode == Mode::MFMA)
+        k_moe_mfma<false><<<mt * (D / 64), 256, 0, st>>>(L->wq, L->h16m, L->list, L->tiles,
+                                                         L->n_tiles, T, K, nullptr, L->out);
+      else
+        k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles,
+                                                      L->n_tiles, L->out);
+      break;
+    case HY3X_STAGE_COMBINE:
+      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+      break;
+  }
+}
+
 int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
   if (!L || !x) return fail(HY3X_E_ARG, "NULL argument");
   if (T < 1 || T > L->max_tokens) return fail(HY3X_E_ARG, "T=%d outside [1,%d]", T, L->max_tokens);
   if (K < 1 || K > KMAX) return fail(HY3X_E_ARG, "K=%d outside [1,8]", K);
   if (!L->router_set) return fail(HY3X_E_STATE, "router not set");
   hipStream_t st = (hipStream_t)stream;
+  auto &c = L->cur;
+  c.x = x;
+  c.T = T;
+  c.K = K;
+  c.scale = scale;
+  if (T == 1 && L->path == 0)
+    c.mode = Mode::DECODE;
+  else if (L->path == 2 || (L->path == 0 && T >= kMfmaMinT))
+    c.mode = Mode::MFMA;
+  else
+    c.mode = Mode::GEMV;
+  c.nt = c.mode == Mode::MFMA ? 64 : 4;
+  c.mt = std::min(max_tiles_for(T, K, c.nt), L->max_tiles_alloc);
   record_stage(L, st, -1);
-  const bool decode = T == 1 && L->path == 0;
-  const bool use_mfma = L->path == 2 || (L->path == 0 && T >= kMfmaMinT);
-  if (T <= kSmallRouterT) {
-    k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias, L->has_bias,
-                                                L->logits, L->sig, L->score, L->s16, L->s32,
-                                                L->trace[0]);
-  } else {
-    k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, L->s16, L->s32);
-    k_router_gemm<<<dim3((T + 31) / 32, E / 64), 256, 0, st>>>(L->s32, L->router, T, L->logits);
-  }
-  if (!decode)
-    k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, scale, L->ids, L->wpre, L->w);
-  record_stage(L, st, HY3X_STAGE_ROUTER);
-  if (decode) {
-    k_gateup_decode<<<(K + 1) * (F / 32), 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
-                                                        scale, L->ids, L->wpre,
-                                                        L->w, L->stats, L->h16, L->trace[1]);
-    record_stage(L, st, HY3X_STAGE_GATEUP);
-    k_down_decode<<<D / 16, 576, 0, st>>>(L->wq, L->h16, L->ids, L->w, K, x, L->trace[2]);
-    record_stage(L, st, HY3X_STAGE_DOWN);
-  } else if (use_mfma) {
-    const int NT = 64;
-    const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
-    k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m);
-    k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts,
-                                  L->stats);
-    record_stage(L, st, HY3X_STAGE_DISPATCH);
-    k_moe_mfma<true><<<mt * (F / 64), 256, 0, st>>>(L->wq, L->s16m, L->list, L->tiles,
-                                                    L->n_tiles, T, K, L->h16m, nullptr);
-    record_stage(L, st, HY3X_STAGE_GATEUP);
-    k_moe_mfma<false><<<mt * (D / 64), 256, 0, st>>>(L->wq, L->h16m, L->list, L->tiles,
-                                                     L->n_tiles, T, K, nullptr, L->out);
-    record_stage(L, st, HY3X_STAGE_DOWN);
-    k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
-    record_stage(L, st, HY3X_STAGE_COMBINE);
-  } else {
-    const int NT = 4;
-    const int mt = std::min(max_tiles_for(T, K, NT), L->max_tiles_alloc);
-    k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, NT, L->list, L->tiles, L->n_tiles, mt, L->counts,
-                                  L->stats);
-    record_stage(L, st, HY3X_STAGE_DISPATCH);
-    k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles, L->n_tiles,
-                                                    T, K, L->h16);
-    record_stage(L, st, HY3X_STAGE_GATEUP);
-    k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles, L->n_tiles,
-                                                  L->out);
-    record_stage(L, st, HY3X_STAGE_DOWN);
-    k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
-    record_stage(L, st, HY3X_STAGE_COMBINE);
+  for (int stage = HY3X_STAGE_ROUTER; stage <= HY3X_STAGE_COMBINE; stage++) {
+    if (c.mode == Mode::DECODE && (stage == HY3X_STAGE_DISPATCH || stage == HY3X_STAGE_COMBINE))
+      continue;
+    launch_stage(L, stage, st);
+    record_stage(L, st, stage);
   }
   if (L->timing) L->n_timed++;
   HIP_TRY(hipGetLastError());
   L->last_T = T;
   L->last_K = K;
   L->last_stream = st;
+  return HY3X_OK;
+}
+
+int hy3x_layer_time_stage(hy3x_layer *L, int stage, int reps, void *stream, float *us) {
+  if (!L || !us || reps < 1) return fail(HY3X_E_ARG, "bad argument");
+  if (stage < HY3X_STAGE_ROUTER || stage > HY3X_STAGE_COMBINE)
+    return fail(HY3X_E_ARG, "stage %d outside [0,4]", stage);
+  if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
+  hipStream_t st = (hipStream_t)stream;
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipEventRecord(e0, st));
+  for (int i = 0; i < reps; i++) launch_stage(L, stage, st);
+  HIP_TRY(hipEventRecord(e1, st));
+  HIP_TRY(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+  HIP_TRY(hipEventDestroy(e0));
+  HIP_TRY(hipEventDestroy(e1));
+  HIP_TRY(hipGetLastError());
+  *us = ms * 1e3f / reps;
   return HY3X_OK;
 }
 

@@ -112,6 +112,14 @@ int hy3x_layer_last_routing(hy3x_layer *layer, int32_t *ids, float *wpre, float 
 int hy3x_layer_set_timing(hy3x_layer *layer, int enable);
 int hy3x_layer_stage_times(hy3x_layer *layer, float *ms, int n_stages, int *n_forwards);
 
+/* Diagnostics: relaunches the kernels of one stage (HY3X_STAGE_*) of the last
+ * forward `reps` times back to back on `stream`, bracketed by two HIP events,
+ * and returns the mean microseconds per launch in *us (synchronises). Inputs
+ * are those of the last forward, so the x buffer it named must still be live;
+ * the down stage of a single-token forward adds its output into x again, so x
+ * is modified. No reference counterpart (measurement only). */
+int hy3x_layer_time_stage(hy3x_layer *layer, int stage, int reps, void *stream, float *us);
+
 /* Device-side counters since the last reset: forwards run and the sum over
  * forwards of the experts touched (shared expert included), i.e. the "U" of
  * the algorithmic byte count. Synchronises the device. */
