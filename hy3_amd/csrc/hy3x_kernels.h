@@ -42,16 +42,17 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
                                                const int4 *, const int32_t *, float *);
 
 template <bool GATEUP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(const uint8_t *wq, const __half *act, const int32_t *list,
-                           const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m,
-                           float *out);
-extern template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const int32_t *,
-                                                 const int4 *, const int32_t *, int, int,
-                                                 __half *, float *);
-extern template __global__ void k_moe_mfma<false>(const uint8_t *, const __half *,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(
+    const uint8_t *wq, const __half *act, const __half *act_sum, const int32_t *list,
+    const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m, float *out);
+extern template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const __half *,
+                                                 const int32_t *, const int4 *, const int32_t *,
+                                                 int, int, __half *, float *);
+extern template __global__ void k_moe_mfma<false>(const uint8_t *, const __half *, const __half *,
                                                   const int32_t *, const int4 *, const int32_t *,
                                                   int, int, __half *, float *);
-__global__ void k_stage_mfma(const float *s32, __half *s16m);
+__global__ void k_stage_mfma(const float *s32, __half *s16m, __half *ssum);
+__global__ void k_hsums(const __half *h16m, __half *hsum);
 
 __global__ void k_synth_q4k(uint8_t *dst, int64_t nblocks, uint64_t seed, uint32_t layer,
                             const float *src);

@@ -32,6 +32,7 @@ struct hy3x_layer {
   int has_bias = 0, router_set = 0;
   float *logits = nullptr, *sig = nullptr, *score = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
   __half *s16 = nullptr, *h16 = nullptr, *s16m = nullptr, *h16m = nullptr;
+  __half *ssum = nullptr, *hsum = nullptr;  // sub-block sums (hi, lo) of s16m / h16m rows
   float *s32 = nullptr;
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
@@ -123,7 +124,7 @@ int hy3x_set_device(int device) {
 int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
   void *ptrs[] = {L->wq, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
-                  L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m,    L->h16,     L->ids,     L->list,
+                  L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m, L->ssum, L->hsum, L->h16,     L->ids,     L->list,
                   L->n_tiles, L->counts, L->tiles, L->tickets, L->stats};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
@@ -157,6 +158,8 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
       (rc = dalloc(&L->s32, T * D * sizeof(float))) ||
       (rc = dalloc(&L->s16m, T * D * sizeof(__half))) ||
       (rc = dalloc(&L->h16m, slots * F * sizeof(__half))) ||
+      (rc = dalloc(&L->ssum, T * (D / 32) * 2 * sizeof(__half))) ||
+      (rc = dalloc(&L->hsum, slots * (F / 32) * 2 * sizeof(__half))) ||
       (rc = dalloc(&L->h16, slots * F * sizeof(__half))) ||
       (rc = dalloc(&L->out, slots * D * sizeof(float))) ||
       (rc = dalloc(&L->list, slots * sizeof(int32_t))) ||
@@ -237,7 +240,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                   L->w);
       break;
     case HY3X_STAGE_DISPATCH:
-      if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m);
+      if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);
       if (c.mode != Mode::DECODE)
         k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, c.nt, L->list, L->tiles, L->n_tiles, mt,
                                       L->counts, L->stats);
@@ -248,8 +251,9 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                             c.scale, L->ids, L->wpre, L->w,
                                                             L->stats, L->h16, L->trace[1]);
       else if (c.mode == Mode::MFMA)
-        k_moe_mfma<true><<<mt * (F / 64), 256, 0, st>>>(L->wq, L->s16m, L->list, L->tiles,
-                                                        L->n_tiles, T, K, L->h16m, nullptr);
+        k_moe_mfma<true><<<mt * (F / 64), 256, 0, st>>>(L->wq, L->s16m, L->ssum, L->list,
+                                                        L->tiles, L->n_tiles, T, K, L->h16m,
+                                                        nullptr);
       else
         k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles,
                                                         L->n_tiles, T, K, L->h16);
@@ -257,9 +261,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
         k_down_decode<<<D / 16, 576, 0, st>>>(L->wq, L->h16, L->ids, L->w, K, x, L->trace[2]);
-      else if (c.mode == Mode::MFMA)
-        k_moe_mfma<false><<<mt * (D / 64), 256, 0, st>>>(L->wq, L->h16m, L->list, L->tiles,
-                                                         L->n_tiles, T, K, nullptr, L->out);
+      else if (c.mode == Mode::MFMA) {
+        k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
+        k_moe_mfma<false><<<mt * (D / 128), 256, 0, st>>>(L->wq, L->h16m, L->hsum, L->list,
+                                                          L->tiles, L->n_tiles, T, K, nullptr,
+                                                          L->out);
+      }
       else
         k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles,
                                                       L->n_tiles, L->out);
