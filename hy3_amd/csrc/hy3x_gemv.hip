@@ -1,7 +1,7 @@
 // hy3x_gemv.hip -- grouped wavefront-reduction GEMV expert kernels (decode)
 // and the weighted combine + residual.
 //
-// Work comes from the device tile list (k_dispatch): a tile is one expert and
+// Work comes from the device tile list (k_dispatch_list): a tile is one expert and
 // up to NT of its slots. The weights of a tile are streamed from HBM once,
 // with 16-byte loads (each lane: the block header + 32 bytes of nibbles), and
 // dotted against the NT staged activations held in registers. Replaces

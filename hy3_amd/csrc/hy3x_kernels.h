@@ -9,12 +9,24 @@ __global__ void k_router_logits(const float *x, const float *norm_w, const float
                                 float *score, __half *s16, float *s32,
                                 unsigned long long *trace);
 __global__ void k_rmsnorm(const float *x, const float *norm_w, __half *s16, float *s32);
-__global__ void k_router_gemm(const float *s32, const float *router, int T, float *logits);
+template <int MT, int ME, int TG, int EG>
+__global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
+                                                     float *logits);
+extern template __global__ void k_router_gemm<4, 4, 4, 8>(const float *, const float *, int,
+                                                          float *);
+extern template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const float *, int,
+                                                          float *);
+extern template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int,
+                                                          float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
                        int32_t *ids, float *wpre, float *wout);
-__global__ void k_dispatch(const int32_t *ids, int T, int K, int NT, int32_t *list, int4 *tiles,
-                           int32_t *n_tiles, int max_tiles, int32_t *counts_out,
-                           unsigned long long *stats);
+__global__ void k_dispatch_clear(int T, uint32_t *bits, int wt, int32_t *dcount);
+__global__ void k_dispatch_mark(const int32_t *ids, int T, int K, uint32_t *bits, int wt,
+                                int32_t *dcount);
+__global__ void k_dispatch_list(const int32_t *ids, int T, int K, int NT, const uint32_t *bits,
+                                int wt, const int32_t *dcount, int32_t *list, int4 *tiles,
+                                int32_t *n_tiles, int max_tiles, int32_t *counts_out,
+                                unsigned long long *stats);
 template <int NT>
 __global__ void k_gateup_gemv(const uint8_t *wq, const __half *s16, const int32_t *list,
                               const int4 *tiles, const int32_t *n_tiles, int T, int K,

@@ -36,7 +36,9 @@ struct hy3x_layer {
   float *s32 = nullptr;
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
-  unsigned *tickets = nullptr;
+  uint32_t *bits = nullptr;    // dispatch: per-expert token bitmaps [E][wt]
+  int32_t *dcount = nullptr;   // dispatch: per-expert slot counts
+  int wt = 0;                  // bitmap words per expert (max_tokens / 32, rounded up)
   unsigned long long *stats = nullptr;
   int max_tiles_alloc = 0;
   int last_T = 0, last_K = 0;
@@ -103,6 +105,10 @@ static int dalloc(P **p, size_t bytes) {
 // Up to this many tokens the router runs as one wave per (expert, token);
 // above it as RMSNorm + LDS-tiled GEMM + per-token top-K.
 constexpr int kSmallRouterT = 8;
+// Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks).
+constexpr int kMidRouterT = 128;
+// Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
+constexpr int kLargeRouterT = 512;
 // From this many tokens the experts run as MFMA grouped GEMMs, below it as
 // wavefront-reduction GEMVs.
 constexpr int kMfmaMinT = 64;
@@ -125,7 +131,7 @@ int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
   void *ptrs[] = {L->wq, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
                   L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m, L->ssum, L->hsum, L->h16,     L->ids,     L->list,
-                  L->n_tiles, L->counts, L->tiles, L->tickets, L->stats};
+                  L->n_tiles, L->counts, L->tiles, L->bits, L->dcount, L->stats};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   for (hipEvent_t ev : L->ev_pool) (void)hipEventDestroy(ev);
@@ -143,6 +149,7 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
   L->max_tokens = max_tokens;
   const size_t T = (size_t)max_tokens, slots = T * (KMAX + 1);
   L->max_tiles_alloc = max_tiles_for(max_tokens, KMAX, 1);
+  L->wt = (max_tokens + 31) / 32;
   int rc = HY3X_OK;
   if ((rc = dalloc(&L->wq, (size_t)(E + 1) * EXPERT_BYTES)) ||
       (rc = dalloc(&L->norm_w, D * sizeof(float))) ||
@@ -158,20 +165,22 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
       (rc = dalloc(&L->s32, T * D * sizeof(float))) ||
       (rc = dalloc(&L->s16m, T * D * sizeof(__half))) ||
       (rc = dalloc(&L->h16m, slots * F * sizeof(__half))) ||
-      (rc = dalloc(&L->ssum, T * (D / 32) * 2 * sizeof(__half))) ||
-      (rc = dalloc(&L->hsum, slots * (F / 32) * 2 * sizeof(__half))) ||
+      (rc = dalloc(&L->ssum, T * (D / 32) * 4 * sizeof(__half))) ||
+      (rc = dalloc(&L->hsum, slots * (F / 32) * 4 * sizeof(__half))) ||
       (rc = dalloc(&L->h16, slots * F * sizeof(__half))) ||
       (rc = dalloc(&L->out, slots * D * sizeof(float))) ||
       (rc = dalloc(&L->list, slots * sizeof(int32_t))) ||
       (rc = dalloc(&L->tiles, (size_t)L->max_tiles_alloc * sizeof(int4))) ||
       (rc = dalloc(&L->n_tiles, sizeof(int32_t))) ||
       (rc = dalloc(&L->counts, (E + 1) * sizeof(int32_t))) ||
-      (rc = dalloc(&L->tickets, T * sizeof(unsigned))) ||
+      (rc = dalloc(&L->bits, (size_t)E * L->wt * sizeof(uint32_t))) ||
+      (rc = dalloc(&L->dcount, E * sizeof(int32_t))) ||
       (rc = dalloc(&L->stats, 2 * sizeof(unsigned long long)))) {
     hy3x_layer_destroy(L);
     return rc;
   }
-  if (hipMemset(L->tickets, 0, T * sizeof(unsigned)) != hipSuccess ||
+  if (hipMemset(L->bits, 0, (size_t)E * L->wt * sizeof(uint32_t)) != hipSuccess ||
+      hipMemset(L->dcount, 0, E * sizeof(int32_t)) != hipSuccess ||
       hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
       hipMemset(L->stats, 0, 2 * sizeof(unsigned long long)) != hipSuccess) {
     hy3x_layer_destroy(L);
@@ -232,8 +241,15 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                     L->s16, L->s32, L->trace[0]);
       } else {
         k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, L->s16, L->s32);
-        k_router_gemm<<<dim3((T + 31) / 32, E / 64), 256, 0, st>>>(L->s32, L->router, T,
-                                                                    L->logits);
+        if (T <= kMidRouterT)
+          k_router_gemm<2, 2, 4, 8><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
+              L->s32, L->router, T, L->logits);
+        else if (T <= kLargeRouterT)
+          k_router_gemm<4, 4, 4, 8><<<dim3((T + 15) / 16, E / 32), 256, 0, st>>>(
+              L->s32, L->router, T, L->logits);
+        else
+          k_router_gemm<8, 4, 4, 8><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
+              L->s32, L->router, T, L->logits);
       }
       if (c.mode != Mode::DECODE)
         k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, L->ids, L->wpre,
@@ -241,9 +257,15 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_DISPATCH:
       if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);
-      if (c.mode != Mode::DECODE)
-        k_dispatch<<<1, 256, 0, st>>>(L->ids, T, K, c.nt, L->list, L->tiles, L->n_tiles, mt,
-                                      L->counts, L->stats);
+      if (c.mode != Mode::DECODE) {
+        k_dispatch_clear<<<(E * ((T + 31) / 32) + 255) / 256, 256, 0, st>>>(T, L->bits, L->wt,
+                                                                           L->dcount);
+        k_dispatch_mark<<<(T * K + 255) / 256, 256, 0, st>>>(L->ids, T, K, L->bits, L->wt,
+                                                             L->dcount);
+        k_dispatch_list<<<E + 1, 256, 0, st>>>(L->ids, T, K, c.nt, L->bits, L->wt, L->dcount,
+                                               L->list, L->tiles, L->n_tiles, mt, L->counts,
+                                               L->stats);
+      }
       break;
     case HY3X_STAGE_GATEUP:
       if (c.mode == Mode::DECODE)

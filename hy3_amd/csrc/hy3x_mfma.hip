@@ -4,68 +4,98 @@
 // and of up (four waves x 16 rows), or 128 rows of down (four waves x 2 x 16
 // rows) -- and up to 64 of its tokens (the dispatch tile list with NT = 64).
 // Per Q4_K block column (256 of K) every lane turns the 8-element runs of its
-// rows that the MFMA A operand needs into exact integers sc*q in fp16,
-// straight from the GGUF bytes (q via the 0x6400 exponent-bias trick, one
-// packed fp16 FMA with the sub-block scale), while the block's activations for
-// the column sit in LDS. v_mfma_f32_16x16x32_f16 accumulates each block in
-// fp32 (one MFMA spans exactly one Q4_K sub-block of 32); d, dmin and the
-// mins are applied per block (see mfma_tile).
+// weight row that the MFMA needs into exact integers sc*q in fp16, straight
+// from the GGUF bytes (q via the 0x6400 exponent-bias trick, one packed fp16
+// FMA with the sub-block scale), while the block's activations for the column
+// sit in LDS. v_mfma_f32_16x16x32_f16 accumulates each block in fp32 (one MFMA
+// spans exactly one Q4_K sub-block of 32); d, dmin and the mins are applied
+// per block (see mfma_tile).
 //
 // Operand layouts (16x16x32): lane l holds A[l%16][8(l/16) .. +7] (row, k),
-// B[8(l/16) .. +7][l%16] (k, token) and D[4(l/16) + i][l%16], i = 0..3. Within
-// each run of 8 the k order is (0,2,1,3,4,6,5,7), the order the nibble unpack
-// produces; activations are staged in that order (perm8).
+// B[8(l/16) .. +7][l%16] (k, column) and D[4(l/16) + i][l%16], i = 0..3. Here
+// A = activations (rows = tokens) and B = weights (columns = weight rows), so
+// a lane's D values all belong to ONE weight row (its own: l%16) and four
+// tokens. Within each run of 8 the k order is (0,2,1,3,4,6,5,7), the order
+// the nibble unpack produces; activations are staged in that order (perm8).
 #include "hy3x_kernels.h"
 #include "hy3x_q4k.h"
 
 namespace hy3x {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));  // 16 bytes as a native vector
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
 constexpr int MT_TOK = 64;      // tokens per tile (dispatch NT)
 constexpr int BT_STRIDE = 264;  // fp16 per staged token row (256 + 8 pad: conflict-free reads)
-constexpr int BM_STRIDE = 24;   // fp16 per staged token sub-block-sum row (16 + 8 pad)
+constexpr int BM_STRIDE = 40;   // fp16 per staged token mins row (32 + 8 pad)
 
-__device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, uint32_t b, uint32_t c) {
-  const h2_t r = __builtin_elementwise_fma(as_h2(a), as_h2(b), as_h2(c));
-  return __builtin_bit_cast(uint32_t, r);
-}
-__device__ __forceinline__ uint32_t h2_splat(float v) {
-  const _Float16 h = (_Float16)v;
-  const h2_t r = {h, h};
-  return __builtin_bit_cast(uint32_t, r);
+__device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, h2_t b, h2_t c) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(as_h2(a), b, c));
 }
 
-// 6-bit scale and min of sub-block j of a Q4_K header (hy3.c:1001-1009).
-__device__ __forceinline__ void scale_min(const u4_t &hdr, int j, uint32_t &sc, uint32_t &m) {
-  const uint32_t s03 = hdr.y, s47 = hdr.z, s811 = hdr.w;
-  if (j < 4) {
-    sc = bfe(s03, 8 * j, 6);
-    m = bfe(s47, 8 * j, 6);
-  } else {
-    sc = bfe(s811, 8 * (j - 4), 4) | (bfe(s03, 8 * (j - 4) + 6, 2) << 4);
-    m = bfe(s811, 8 * (j - 4) + 4, 4) | (bfe(s47, 8 * (j - 4) + 6, 2) << 4);
-  }
+// The 6-bit scales and mins of a Q4_K block (hy3.c:1001-1009) as bytes:
+// sc[0] = sc_0..3, sc[1] = sc_4..7, mn[0] = m_0..3, mn[1] = m_4..7.
+struct Scales6 {
+  uint32_t sc[2], mn[2];
+};
+__device__ __forceinline__ Scales6 unpack_scales(const u4_t &h) {
+  // j < 4: sc_j = s[j] & 63, m_j = s[j+4] & 63
+  // j >= 4: sc_j = (s[j+4] & 15) | (s[j-4] >> 6) << 4, m_j = (s[j+4] >> 4) | (s[j] >> 6) << 4
+  Scales6 r;
+  r.sc[0] = h.y & 0x3F3F3F3Fu;
+  r.mn[0] = h.z & 0x3F3F3F3Fu;
+  r.sc[1] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+  r.mn[1] = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+  return r;
 }
 
-// A operand for sub-block 2p (hi = false) or 2p+1 (hi = true) with scale sc:
-// the exact integers sc*q in fp16 (sc*q <= 945), from the 8 bytes
-// qs[32p + 8g .. +7]. (1024 + q)*sc - 1024*sc is one fused multiply-add whose
-// exact result is representable, so it is exact.
-__device__ __forceinline__ h8_t dequant_a(u2_t q, bool hi, uint32_t sc) {
-  const uint32_t mag = 0x64006400u, mask = 0x000F000Fu;
-  const uint32_t sc2 = h2_splat((float)sc), nb2 = h2_splat(-1024.0f * (float)sc);
-  const int sh = hi ? 4 : 0;
-  u4_t p;
-  p.x = pk_fma_f16(and_or(q.x >> sh, mask, mag), sc2, nb2);
-  p.y = pk_fma_f16(and_or(q.x >> (8 + sh), mask, mag), sc2, nb2);
-  p.z = pk_fma_f16(and_or(q.y >> sh, mask, mag), sc2, nb2);
-  p.w = pk_fma_f16(and_or(q.y >> (8 + sh), mask, mag), sc2, nb2);
-  return __builtin_bit_cast(h8_t, p);
+// fp16 pair (byte J0 of w, byte J1 of w) (values <= 63): the bytes go into the
+// mantissa of 1024.0, then 1024 is subtracted (both steps exact).
+template <int J0, int J1>
+__device__ __forceinline__ h2_t bytes_h2(uint32_t w) {
+  constexpr uint32_t sel = 0x0C000C00u | ((uint32_t)J1 << 16) | (uint32_t)J0;  // 0x0C: zero byte
+  const uint32_t v = __builtin_amdgcn_perm(w, w, sel) | 0x64006400u;
+  return as_h2(v) + (h2_t){(_Float16)-1024.0f, (_Float16)-1024.0f};
+}
+
+// Weight operands of sub-blocks 2p (lo) and 2p+1 (hi) from the 8 bytes
+// qs[32p + 8g .. +7] of this lane's row: the exact integers sc*q in fp16
+// (sc*q <= 945). sc = (sc_lo, sc_hi). Low nibbles: 0x6400 | q = 1024 + q,
+// times sc_lo, minus 1024 sc_lo. High nibbles, left in place: 0x6400 | 16q =
+// 1024 + 16q, times sc_hi/16, minus 64 sc_hi. Each is one fused multiply-add
+// whose exact result is representable, so it is exact.
+__device__ __forceinline__ void dequant_pair(u2_t q, h2_t sc, h8_t &w_lo, h8_t &w_hi) {
+  const uint32_t mag = 0x64006400u, m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
+  const h2_t mul = sc * (h2_t){(_Float16)1.0f, (_Float16)0.0625f};     // (sc_lo, sc_hi/16)
+  const h2_t add = sc * (h2_t){(_Float16)-1024.0f, (_Float16)-64.0f};  // (-1024 sc_lo, -64 sc_hi)
+  const h2_t ml = {mul[0], mul[0]}, al = {add[0], add[0]};
+  const h2_t mh = {mul[1], mul[1]}, ah = {add[1], add[1]};
+  const uint32_t x8 = q.x >> 8, y8 = q.y >> 8;
+  u4_t lo, hi;
+  lo.x = pk_fma_f16(and_or(q.x, m_lo, mag), ml, al);
+  lo.y = pk_fma_f16(and_or(x8, m_lo, mag), ml, al);
+  lo.z = pk_fma_f16(and_or(q.y, m_lo, mag), ml, al);
+  lo.w = pk_fma_f16(and_or(y8, m_lo, mag), ml, al);
+  hi.x = pk_fma_f16(and_or(q.x, m_hi, mag), mh, ah);
+  hi.y = pk_fma_f16(and_or(x8, m_hi, mag), mh, ah);
+  hi.z = pk_fma_f16(and_or(q.y, m_hi, mag), mh, ah);
+  hi.w = pk_fma_f16(and_or(y8, m_hi, mag), mh, ah);
+  w_lo = __builtin_bit_cast(h8_t, lo);
+  w_hi = __builtin_bit_cast(h8_t, hi);
+}
+
+// -dmin * m_j for sub-blocks j = 2g and 2g+1 of this lane's row, each split
+// exactly into two fp16 parts (dmin: 11 significant bits, m: 6, so the
+// product is exact in fp32 and hi + lo carries it to 22 bits), laid out for
+// the mins MFMA: k = 4j' + c, c = (hi, hi, lo, lo) against the staged
+// activation sums (Sh, Sl, Sh, Sl): the four cross products of the two splits.
+__device__ __forceinline__ h8_t mins_operand(float dmin, uint32_t m2) {
+  const float v0 = -dmin * (float)(m2 & 0xFFu), v1 = -dmin * (float)((m2 >> 8) & 0xFFu);
+  const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+  const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+  return (h8_t){h0, h0, l0, l0, h1, h1, l1, l1};
 }
 
 template <bool GATEUP>
@@ -82,17 +112,17 @@ struct MfmaCfg {
 
 struct MfmaSmem {
   _Float16 bt[2][MT_TOK][BT_STRIDE];  // activations of one block column (double-buffered)
-  _Float16 bm[2][MT_TOK][BM_STRIDE];  // their sub-block sums as (hi, lo) fp16 pairs
+  _Float16 bm[2][MT_TOK][BM_STRIDE];  // their sub-block sums as (Sh, Sl, Sh, Sl) per sub-block
   int32_t slot[MT_TOK], arow[MT_TOK];
 };
 
 // One work tile with NTT token tiles of 16 (n <= 16 * NTT tokens).
 //
-// Per block column: Dblk = sum over the 8 sub-blocks of MFMA(sc*q, x) (exact
-// integer weights, fp16 activations, fp32 accumulation), Dmin = MFMA of the
-// 6-bit mins against the tokens' sub-block sums of x (each sum carried as two
-// fp16 parts), and acc += d * Dblk - dmin * Dmin with d, dmin of the D rows in
-// fp32 -- the Q4_K identity sum_k w_k x_k = d sum_j sc_j sum_{k in j} q_k x_k
+// Per block column, for each (token tile, weight row group, matrix):
+//   Dblk = sum over the 8 sub-blocks of MFMA(x, sc*q)   (exact integer weights)
+//   acc = MFMA(S, -dmin*m, acc)                         (mins term)
+//   acc += d * Dblk                                     (fp32, d of the lane's row)
+// -- the Q4_K identity sum_k w_k x_k = d sum_j sc_j sum_{k in j} q_k x_k
 // - dmin sum_j m_j sum_{k in j} x_k (hy3.c:1036-1037).
 //
 // Pipeline: the weights (registers) and activations (registers, then the LDS
@@ -107,7 +137,7 @@ __device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restric
   using C = MfmaCfg<GATEUP>;
   constexpr int RG = C::RG, NMAT = C::NMAT, NKB = C::NKB, KD = C::KD;
   constexpr int NTOK = 16 * NTT;
-  constexpr int BU = NTOK / 8;  // B uint4 per thread: tokens (tid >> 5) + 8u
+  constexpr int BU = NTOK / 8;  // activation uint4 per thread: tokens (tid >> 5) + 8u
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, g = lane >> 4;
 
@@ -119,10 +149,10 @@ __device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restric
       abase[rg][m] = wq + (size_t)e * EXPERT_BYTES + (size_t)(GATEUP ? m : 2) * MAT_BYTES +
                      (size_t)(rt * C::TROWS + 16 * (wave * RG + rg) + lr) * NKB * QB;
 
-  // B staging: thread tid moves 16-byte chunk (tid & 31) of tokens (tid >> 5) + 8u,
-  // and threads below 2 * NTOK half of one token's sub-block sums. Token slots
-  // past n re-load token 0's row (its D columns are never stored), so every
-  // prefetch register is written unconditionally.
+  // Activation staging: thread tid moves 16-byte chunk (tid & 31) of tokens
+  // (tid >> 5) + 8u, and threads below 4 * NTOK a quarter of one token's sums
+  // row. Token slots past n re-load token 0's row (their D rows are never
+  // stored), so every prefetch register is written unconditionally.
   const int bc = tid & 31, bt0 = tid >> 5;
   const int arow0 = sm.arow[0];
   const u4_t *bsrc[BU];
@@ -131,11 +161,11 @@ __device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restric
     const int ar = sm.arow[bt0 + 8 * u];
     bsrc[u] = reinterpret_cast<const u4_t *>(act + (size_t)(ar >= 0 ? ar : arow0) * KD) + bc;
   }
-  const bool s_mover = tid < 2 * NTOK;
-  const int ars = s_mover ? sm.arow[tid >> 1] : -1;
+  const bool s_mover = tid < 4 * NTOK;
+  const int ars = s_mover ? sm.arow[tid >> 2] : -1;
   const u4_t *ssrc =
-      reinterpret_cast<const u4_t *>(act_sum + (size_t)(ars >= 0 ? ars : arow0) * C::NSUB * 2) +
-      (tid & 1);
+      reinterpret_cast<const u4_t *>(act_sum + (size_t)(ars >= 0 ? ars : arow0) * C::NSUB * 4) +
+      (tid & 3);
 
   u4_t bnext[BU];
   u4_t snext = {0u, 0u, 0u, 0u};
@@ -156,22 +186,19 @@ __device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restric
     }
 
   f4_t acc[RG][NMAT][NTT];
+  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-      for (int t = 0; t < NTT; t++) acc[rg][m][t] = (f4_t){0.f, 0.f, 0.f, 0.f};
-  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-  h8_t zero8;
-#pragma unroll
-  for (int u = 0; u < 8; u++) zero8[u] = (_Float16)0.0f;
+      for (int t = 0; t < NTT; t++) acc[rg][m][t] = zero4;
 
   for (int kb = 0; kb < NKB; kb++) {
     const int buf = kb & 1;
 #pragma unroll
     for (int u = 0; u < BU; u++) *reinterpret_cast<u4_t *>(&sm.bt[buf][bt0 + 8 * u][8 * bc]) = bnext[u];
-    if (s_mover) *reinterpret_cast<u4_t *>(&sm.bm[buf][tid >> 1][8 * (tid & 1)]) = snext;
+    if (s_mover) *reinterpret_cast<u4_t *>(&sm.bm[buf][tid >> 2][8 * (tid & 3)]) = snext;
     u4_t hdr[RG][NMAT];
     u2_t qv[RG][NMAT][4];
 #pragma unroll
@@ -187,7 +214,7 @@ __device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restric
     const int kn = kb + 1 < NKB ? kb + 1 : kb;
 #pragma unroll
     for (int u = 0; u < BU; u++) bnext[u] = bsrc[u][kn * (QK / 8)];
-    if (s_mover) snext = ssrc[kn * 2];
+    if (s_mover) snext = ssrc[kn * 4];
 #pragma unroll
     for (int rg = 0; rg < RG; rg++)
 #pragma unroll
@@ -198,86 +225,83 @@ __device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restric
         for (int p = 0; p < 4; p++)
           qnext[rg][m][p] = *reinterpret_cast<const u2_t *>(bp + 16 + 32 * p + 8 * g);
       }
+
+    Scales6 sc6[RG][NMAT];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+      for (int m = 0; m < NMAT; m++) sc6[rg][m] = unpack_scales(hdr[rg][m]);
     f4_t dblk[RG][NMAT][NTT];
 #pragma unroll
-    for (int sb = 0; sb < 8; sb++) {
-      h8_t a[RG][NMAT];
+    for (int p = 0; p < 4; p++) {  // sub-blocks 2p and 2p+1
+      h8_t wf[2][RG][NMAT];
 #pragma unroll
       for (int rg = 0; rg < RG; rg++)
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-          uint32_t sc, mn;
-          scale_min(hdr[rg][m], sb, sc, mn);
-          a[rg][m] = dequant_a(qv[rg][m][sb >> 1], sb & 1, sc);
+          const uint32_t w = sc6[rg][m].sc[p >> 1];
+          const h2_t sc = (p & 1) ? bytes_h2<2, 3>(w) : bytes_h2<0, 1>(w);
+          dequant_pair(qv[rg][m][p], sc, wf[0][rg][m], wf[1][rg][m]);
         }
 #pragma unroll
-      for (int t = 0; t < NTT; t++) {
-        const h8_t b = *reinterpret_cast<const h8_t *>(&sm.bt[buf][16 * t + lr][32 * sb + 8 * g]);
+      for (int h = 0; h < 2; h++) {
+        const int sb = 2 * p + h;
 #pragma unroll
-        for (int rg = 0; rg < RG; rg++)
+        for (int t = 0; t < NTT; t++) {
+          const h8_t x =
+              *reinterpret_cast<const h8_t *>(&sm.bt[buf][16 * t + lr][32 * sb + 8 * g]);
 #pragma unroll
-          for (int m = 0; m < NMAT; m++)
-            dblk[rg][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                a[rg][m], b, sb == 0 ? zero4 : dblk[rg][m][t], 0, 0, 0);
+          for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+              dblk[rg][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  x, wf[h][rg][m], sb == 0 ? zero4 : dblk[rg][m][t], 0, 0, 0);
+        }
       }
     }
-    // mins term and per-block scales
+    // per-block scale d (of this lane's row) and the mins MFMA
+    h8_t sv[NTT];
+#pragma unroll
+    for (int t = 0; t < NTT; t++)
+      sv[t] = *reinterpret_cast<const h8_t *>(&sm.bm[buf][16 * t + lr][8 * g]);
 #pragma unroll
     for (int rg = 0; rg < RG; rg++)
 #pragma unroll
       for (int m = 0; m < NMAT; m++) {
-        const u4_t h = hdr[rg][m];
-        const float d_own = fp16_quirk(h.x & 0xffffu), dm_own = fp16_quirk(h.x >> 16);
-        float dr[4], dmr[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {  // d, dmin of D rows 4g + i live in lanes 4g + i
-          dr[i] = __shfl(d_own, 4 * g + i, 64);
-          dmr[i] = __shfl(dm_own, 4 * g + i, 64);
-        }
-        h8_t am = zero8;  // A of the mins MFMA: k = 2j + h (h: hi/lo part), k < 16
-        if (g < 2) {
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            uint32_t sc, mn;
-            scale_min(h, 4 * g + u, sc, mn);
-            am[2 * u] = (_Float16)(float)mn;
-            am[2 * u + 1] = (_Float16)(float)mn;
-          }
-        }
+        const u4_t hd = hdr[rg][m];
+        const float d = fp16_quirk(hd.x & 0xffffu), dmin = fp16_quirk(hd.x >> 16);
+        // m_{2g}, m_{2g+1}: bytes 2(g & 1), 2(g & 1) + 1 of mn[g >> 1]
+        const uint32_t mw = (g >> 1) ? sc6[rg][m].mn[1] : sc6[rg][m].mn[0];
+        const h8_t mo = mins_operand(dmin, (g & 1) ? (mw >> 16) : mw);
 #pragma unroll
         for (int t = 0; t < NTT; t++) {
-          const h8_t bmv =
-              g < 2 ? *reinterpret_cast<const h8_t *>(&sm.bm[buf][16 * t + lr][8 * g]) : zero8;
-          const f4_t dmin4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bmv, zero4, 0, 0, 0);
+          acc[rg][m][t] =
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(sv[t], mo, acc[rg][m][t], 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; i++)
-            acc[rg][m][t][i] = __builtin_fmaf(dr[i], dblk[rg][m][t][i],
-                                              __builtin_fmaf(-dmr[i], dmin4[i], acc[rg][m][t][i]));
+            acc[rg][m][t][i] = __builtin_fmaf(d, dblk[rg][m][t][i], acc[rg][m][t][i]);
         }
       }
   }
-  // epilogue: lane holds D[4g + i][lr] of token tile t, row group rg
+  // epilogue: lane holds D[token 16t + 4g + i][row] for its own weight row
 #pragma unroll
-  for (int t = 0; t < NTT; t++) {
-    const int tok = 16 * t + lr;
-    if (tok < n) {
-      const int slot = sm.slot[tok];
+  for (int rg = 0; rg < RG; rg++) {
+    const int r = rt * C::TROWS + 16 * (wave * RG + rg) + lr;
 #pragma unroll
-      for (int rg = 0; rg < RG; rg++) {
-        const int r0 = rt * C::TROWS + 16 * (wave * RG + rg) + 4 * g;
-        if constexpr (GATEUP) {
-          float hv[4];
+    for (int t = 0; t < NTT; t++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) hv[i] = silu(acc[rg][0][t][i]) * acc[rg][NMAT - 1][t][i];
-          // rows r0 .. r0+3 sit at perm8 positions r0, r0+2, r0+1, r0+3
-          const h4_t v = {(_Float16)hv[0], (_Float16)hv[2], (_Float16)hv[1], (_Float16)hv[3]};
-          *reinterpret_cast<h4_t *>(&h16m[(size_t)slot * F + r0]) = v;
-        } else {
-          *reinterpret_cast<float4 *>(&out[(size_t)slot * D + r0]) =
-              make_float4(acc[rg][0][t][0], acc[rg][0][t][1], acc[rg][0][t][2], acc[rg][0][t][3]);
+      for (int i = 0; i < 4; i++) {
+        const int tok = 16 * t + 4 * g + i;
+        if (tok < n) {
+          const int slot = sm.slot[tok];
+          if constexpr (GATEUP) {
+            h16m[(size_t)slot * F + perm8(r)] =
+                __float2half(silu(acc[rg][0][t][i]) * acc[rg][1][t][i]);
+          } else {
+            out[(size_t)slot * D + r] = acc[rg][0][t][i];
+          }
         }
       }
-    }
   }
 }
 
@@ -290,10 +314,11 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return x * q + (x < r ? x : r) + i;
 }
 
-// Grouped GEMM over the tile list. GATEUP: A = gate and up rows of the expert
-// (K = 4096), B = staged s, epilogue h = silu(g) * u -> h16m[slot][perm8(row)]
-// (fp16). Otherwise A = down rows (K = 1536), B = h16m, out[slot][row] fp32.
-// act_sum: sub-block sums of each activation row as (hi, lo) fp16 pairs.
+// Grouped GEMM over the tile list. GATEUP: weights = gate and up rows of the
+// expert (K = 4096), activations = staged s, epilogue h = silu(g) * u ->
+// h16m[slot][perm8(row)] (fp16). Otherwise weights = down rows (K = 1536),
+// activations = h16m, out[slot][row] fp32. act_sum: sub-block sums of each
+// activation row as (Sh, Sl, Sh, Sl) fp16 quadruples.
 template <bool GATEUP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(
     const uint8_t *__restrict__ wq, const __half *__restrict__ act,
@@ -323,8 +348,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   }
 }
 
-// Sub-block sums of one fp16 row of n32 * 32 values, as (hi, lo) fp16 pairs:
-// hi = fp16(sum), lo = fp16(sum - hi). One lane per sub-block.
+// Sub-block sums of one fp16 row of n32 * 32 values, as (Sh, Sl, Sh, Sl) with
+// Sh = fp16(sum), Sl = fp16(sum - Sh). One lane per sub-block.
 __device__ __forceinline__ void row_subsums(const __half *__restrict__ row, int n32,
                                             __half *__restrict__ dst) {
   for (int j = threadIdx.x; j < n32; j += blockDim.x) {
@@ -344,12 +369,13 @@ __device__ __forceinline__ void row_subsums(const __half *__restrict__ row, int 
     const _Float16 hi = (_Float16)sum;
     const _Float16 lo = (_Float16)(sum - (float)hi);
     const h2_t r = {hi, lo};
-    *reinterpret_cast<h2_t *>(dst + 2 * j) = r;
+    *reinterpret_cast<h2_t *>(dst + 4 * j) = r;
+    *reinterpret_cast<h2_t *>(dst + 4 * j + 2) = r;
   }
 }
 
-// fp16 copy of s in the MFMA run order (perm8) for the gate/up B operand, and
-// its 128 sub-block sums.
+// fp16 copy of s in the MFMA run order (perm8) for the gate/up activations,
+// and its 128 sub-block sums.
 __global__ __launch_bounds__(256) void k_stage_mfma(const float *__restrict__ s32,
                                                     __half *__restrict__ s16m,
                                                     __half *__restrict__ ssum) {
@@ -357,14 +383,14 @@ __global__ __launch_bounds__(256) void k_stage_mfma(const float *__restrict__ s3
   for (int j = threadIdx.x; j < D; j += 256)
     s16m[(size_t)t * D + perm8(j)] = __float2half(s32[(size_t)t * D + j]);
   __syncthreads();
-  row_subsums(s16m + (size_t)t * D, D / 32, ssum + (size_t)t * (D / 32) * 2);
+  row_subsums(s16m + (size_t)t * D, D / 32, ssum + (size_t)t * (D / 32) * 4);
 }
 
 // The 48 sub-block sums of every h row (down-GEMM mins operand); one wave per slot.
 __global__ __launch_bounds__(64) void k_hsums(const __half *__restrict__ h16m,
                                               __half *__restrict__ hsum) {
   const int slot = blockIdx.x;
-  row_subsums(h16m + (size_t)slot * F, F / 32, hsum + (size_t)slot * (F / 32) * 2);
+  row_subsums(h16m + (size_t)slot * F, F / 32, hsum + (size_t)slot * (F / 32) * 4);
 }
 
 template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const __half *,

@@ -154,72 +154,95 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
   }
 }
 
-// logits[T x 192] = s[T x 4096] . router^T, block tile 32 tokens x 64 experts,
-// thread tile 4 tokens x 2 experts x 8 chains. K is walked in chunks of 64
-// elements (8 chain steps) staged in LDS; every chain runs i ascending.
+// logits[T x 192] = s[T x 4096] . router^T for T > 8, in the router's fixed
+// summation order: 8 chains per output, chain v = fmaf over elements 8i + v
+// with i ascending, then tree8 (the order of hy3.c's vectorised fast-math
+// mul_mat_f32, hy3.c:1076-1085). A thread runs ONE chain v for an MT x ME
+// micro-tile of (token, expert) outputs; the 8 chains of a micro-tile sit in
+// 8 neighbouring lanes and are combined with tree8_lanes. Block tile:
+// TT = MT*TG tokens x TE = ME*EG experts, K walked in chunks of KC staged
+// k-major in LDS (double-buffered, next chunk prefetched into registers).
+template <int MT, int ME, int TG, int EG>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s32,
                                                      const float *__restrict__ router, int T,
                                                      float *__restrict__ logits) {
-  constexpr int TT = 32, TE = 64, KC = 64;
-  __shared__ float4 sl[TT][KC / 4 + 1], wl[TE][KC / 4 + 1];
+  static_assert(8 * TG * EG == 256, "256 threads");
+  constexpr int TT = MT * TG, TE = ME * EG, KC = 128;
+  constexpr int SP = TT + 4, WP = TE + 4;        // padded LDS rows (floats)
+  constexpr int NS = TT * KC / 4 / 256, NW = TE * KC / 4 / 256;  // float4 per thread
+  static_assert(NS >= 1 && NW >= 1, "staging split");
+  __shared__ float sl[2][KC][SP], wl[2][KC][WP];
   const int t0 = blockIdx.x * TT, e0 = blockIdx.y * TE;
-  const int tid = threadIdx.x, tg = tid & 7, eg = tid >> 3;  // 8 token groups x 32 expert groups
-  float acc[4][2][8];
+  const int tid = threadIdx.x, v = tid & 7, mt = tid >> 3, tg = mt % TG, eg = mt / TG;
+  float4 sn[NS], wn[NW];
+  auto fetch = [&](int k0) {
 #pragma unroll
-  for (int a = 0; a < 4; a++)
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-      for (int v = 0; v < 8; v++) acc[a][b][v] = 0.0f;
-  for (int k0 = 0; k0 < D; k0 += KC) {
-    // stage: 32x64 s (512 float4) and 64x64 router (1024 float4)
-    for (int q = tid; q < TT * KC / 4; q += 256) {
-      const int rr = q / (KC / 4), cc = q % (KC / 4), tt = t0 + rr;
-      sl[rr][cc] = tt < T ? reinterpret_cast<const float4 *>(s32 + (size_t)tt * D + k0)[cc]
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < NS; u++) {
+      const int q = tid + 256 * u, r = q % TT, c = q / TT, tt = t0 + r;
+      sn[u] = tt < T ? reinterpret_cast<const float4 *>(s32 + (size_t)tt * D + k0)[c]
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int q = tid; q < TE * KC / 4; q += 256) {
-      const int rr = q / (KC / 4), cc = q % (KC / 4);
-      wl[rr][cc] = reinterpret_cast<const float4 *>(router + (size_t)(e0 + rr) * D + k0)[cc];
+#pragma unroll
+    for (int u = 0; u < NW; u++) {
+      const int q = tid + 256 * u, r = q % TE, c = q / TE;
+      wn[u] = reinterpret_cast<const float4 *>(router + (size_t)(e0 + r) * D + k0)[c];
     }
-    __syncthreads();
+  };
+  auto stage = [&](int buf) {
 #pragma unroll
-    for (int ii = 0; ii < KC / 8; ii++) {  // chain step: elements 8ii .. 8ii+7 of the chunk
-      float4 sa[4][2], wb[2][2];
-#pragma unroll
-      for (int a = 0; a < 4; a++) {
-        sa[a][0] = sl[tg + 8 * a][2 * ii];
-        sa[a][1] = sl[tg + 8 * a][2 * ii + 1];
-      }
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        wb[b][0] = wl[eg + 32 * b][2 * ii];
-        wb[b][1] = wl[eg + 32 * b][2 * ii + 1];
-      }
-#pragma unroll
-      for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-          acc[a][b][0] = __builtin_fmaf(wb[b][0].x, sa[a][0].x, acc[a][b][0]);
-          acc[a][b][1] = __builtin_fmaf(wb[b][0].y, sa[a][0].y, acc[a][b][1]);
-          acc[a][b][2] = __builtin_fmaf(wb[b][0].z, sa[a][0].z, acc[a][b][2]);
-          acc[a][b][3] = __builtin_fmaf(wb[b][0].w, sa[a][0].w, acc[a][b][3]);
-          acc[a][b][4] = __builtin_fmaf(wb[b][1].x, sa[a][1].x, acc[a][b][4]);
-          acc[a][b][5] = __builtin_fmaf(wb[b][1].y, sa[a][1].y, acc[a][b][5]);
-          acc[a][b][6] = __builtin_fmaf(wb[b][1].z, sa[a][1].z, acc[a][b][6]);
-          acc[a][b][7] = __builtin_fmaf(wb[b][1].w, sa[a][1].w, acc[a][b][7]);
-        }
+    for (int u = 0; u < NS; u++) {  // neighbouring lanes write neighbouring words
+      const int q = tid + 256 * u, r = q % TT, c = q / TT;
+      sl[buf][4 * c + 0][r] = sn[u].x;
+      sl[buf][4 * c + 1][r] = sn[u].y;
+      sl[buf][4 * c + 2][r] = sn[u].z;
+      sl[buf][4 * c + 3][r] = sn[u].w;
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NW; u++) {
+      const int q = tid + 256 * u, r = q % TE, c = q / TE;
+      wl[buf][4 * c + 0][r] = wn[u].x;
+      wl[buf][4 * c + 1][r] = wn[u].y;
+      wl[buf][4 * c + 2][r] = wn[u].z;
+      wl[buf][4 * c + 3][r] = wn[u].w;
+    }
+  };
+  float acc[MT][ME];
+#pragma unroll
+  for (int a = 0; a < MT; a++)
+#pragma unroll
+    for (int b = 0; b < ME; b++) acc[a][b] = 0.0f;
+  fetch(0);
+  for (int k0 = 0, it = 0; k0 < D; k0 += KC, it++) {
+    const int buf = it & 1;
+    stage(buf);
+    __syncthreads();  // buf staged; the other buffer is no longer read
+    if (k0 + KC < D) fetch(k0 + KC);
+#pragma unroll 4
+    for (int ii = 0; ii < KC / 8; ii++) {
+      const int k = 8 * ii + v;
+      float sv[MT], wv[ME];
+#pragma unroll
+      for (int a = 0; a < MT; a++) sv[a] = sl[buf][k][MT * tg + a];
+#pragma unroll
+      for (int b = 0; b < ME; b++) wv[b] = wl[buf][k][ME * eg + b];
+#pragma unroll
+      for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int b = 0; b < ME; b++) acc[a][b] = __builtin_fmaf(wv[b], sv[a], acc[a][b]);
+    }
   }
 #pragma unroll
-  for (int a = 0; a < 4; a++)
+  for (int a = 0; a < MT; a++)
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-      const int tt = t0 + tg + 8 * a, ee = e0 + eg + 32 * b;
-      if (tt < T) logits[(size_t)tt * E + ee] = tree8(acc[a][b]);
+    for (int b = 0; b < ME; b++) {
+      const float lg = tree8_lanes(acc[a][b], v);
+      const int tt = t0 + MT * tg + a, ee = e0 + ME * eg + b;
+      if (v == 0 && tt < T) logits[(size_t)tt * E + ee] = lg;
     }
 }
+template __global__ void k_router_gemm<4, 4, 4, 8>(const float *, const float *, int, float *);
+template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int, float *);
+template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const float *, int, float *);
 
 // Routing of one token per block (large-T path): sigmoid and scores of the
 // 192 logits, then the top-K.
@@ -240,10 +263,11 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
              sc_l, sg_l, scratch_l);
 }
 
-// Device dispatch: per-expert slot lists and the work-tile list, one block of
-// 256 threads (four waves; expert e is handled by thread e).
+// Device dispatch: per-expert slot lists and the work-tile list.
 // Slots: s < T*K is (token s/K, rank s%K) of a routed expert; s = T*K + t is
-// token t of the shared expert (index E), which every token uses.
+// token t of the shared expert (index E), which every token uses. Each
+// expert's slots are listed in token order, so the lists (and the tiles, and
+// every result computed from them) do not depend on scheduling.
 // tiles[i] = {expert, first list index, count <= NT, 0}.
 __device__ __forceinline__ int block_exclusive_scan256(int v, int *tmp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -261,46 +285,90 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int *tmp) {
   return base + incl - v;
 }
 
-__global__ __launch_bounds__(256) void k_dispatch(const int32_t *__restrict__ ids, int T, int K,
-                                                  int NT, int32_t *__restrict__ list,
-                                                  int4 *__restrict__ tiles,
-                                                  int32_t *__restrict__ n_tiles, int max_tiles,
-                                                  int32_t *__restrict__ counts_out,
-                                                  unsigned long long *__restrict__ stats) {
-  __shared__ int cnt[256], cur[256], tmp[8];
-  const int tid = threadIdx.x, n = T * K;
-  cnt[tid] = 0;
-  cur[tid] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += 256) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
-  const int c = tid < E ? cnt[tid] : (tid == E ? T : 0);
+// Step 0: clear the E x ceil(T/32) bitmap words and the counters of step 1
+// (a fill kernel, so the whole forward can be captured in a graph).
+__global__ __launch_bounds__(256) void k_dispatch_clear(int T, uint32_t *__restrict__ bits, int wt,
+                                                        int32_t *__restrict__ dcount) {
+  const int nw = (T + 31) >> 5;
+  const int f = blockIdx.x * 256 + threadIdx.x;
+  if (f < E * nw) bits[(f / nw) * wt + f % nw] = 0u;
+  if (f < E) dcount[f] = 0;
+}
+
+// Step 1, one thread per routed slot: bit t of expert e's token bitmap
+// (bits[e * wt + t / 32]) and expert e's count. Both results are independent
+// of the order of the atomics.
+__global__ __launch_bounds__(256) void k_dispatch_mark(const int32_t *__restrict__ ids, int T,
+                                                       int K, uint32_t *__restrict__ bits, int wt,
+                                                       int32_t *__restrict__ dcount) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= T * K) return;
+  const int e = ids[i], t = i / K;
+  if (e < 0 || e >= E) return;
+  atomicOr(&bits[(size_t)e * wt + (t >> 5)], 1u << (t & 31));
+  atomicAdd(&dcount[e], 1);
+}
+
+// Step 2, one block per expert (E + 1 blocks, the last is the shared expert):
+// list offset and first tile from exclusive scans of all counts, the expert's
+// tiles, and its slots in token order from its bitmap (popcount prefix sums).
+// Block E also writes the tile count, the per-expert counts and the stats.
+__global__ __launch_bounds__(256) void k_dispatch_list(
+    const int32_t *__restrict__ ids, int T, int K, int NT, const uint32_t *__restrict__ bits,
+    int wt, const int32_t *__restrict__ dcount, int32_t *__restrict__ list,
+    int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles, int max_tiles,
+    int32_t *__restrict__ counts_out, unsigned long long *__restrict__ stats) {
+  __shared__ int tmp[8], off_l, toff_l;
+  const int e = blockIdx.x, tid = threadIdx.x;
+  const int c = tid < E ? dcount[tid] : (tid == E ? T : 0);
   const int off = block_exclusive_scan256(c, tmp);
   const int nt = (c + NT - 1) / NT;
   const int toff = block_exclusive_scan256(nt, tmp);
-  const int active = block_exclusive_scan256(c > 0 ? 1 : 0, tmp);
-  if (tid == 255) {
-    *n_tiles = toff < max_tiles ? toff : max_tiles;
-    if (stats) {  // forwards, experts touched (shared included)
-      stats[0] += 1ull;
-      stats[1] += (unsigned long long)active;
+  if (tid == e) {
+    off_l = off;
+    toff_l = toff;
+  }
+  if (e == E) {
+    const int active = block_exclusive_scan256(c > 0 ? 1 : 0, tmp);
+    if (tid == 255) {
+      *n_tiles = toff < max_tiles ? toff : max_tiles;
+      if (stats) {  // forwards, experts touched (shared included)
+        stats[0] += 1ull;
+        stats[1] += (unsigned long long)active;
+      }
     }
+    if (counts_out && tid <= E) counts_out[tid] = c;
   }
-  __shared__ int offs[256];
-  offs[tid] = off;
   __syncthreads();
-  for (int i = tid; i < n; i += 256) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) list[offs[e] + atomicAdd(&cur[e], 1)] = i;
+  const int eoff = off_l, etoff = toff_l;
+  const int ce = e < E ? dcount[e] : T;
+  for (int j = tid; j * NT < ce; j += 256)
+    if (etoff + j < max_tiles) tiles[etoff + j] = make_int4(e, eoff + j * NT, min(NT, ce - j * NT), 0);
+  if (e == E) {
+    for (int t = tid; t < T; t += 256) list[eoff + t] = T * K + t;
+    return;
   }
-  for (int t = tid; t < T; t += 256) list[offs[E] + t] = n + t;
-  if (tid <= E) {
-    if (counts_out) counts_out[tid] = c;
-    for (int j = 0, ti = toff; j * NT < c && ti < max_tiles; j++, ti++)
-      tiles[ti] = make_int4(tid, off + j * NT, min(NT, c - j * NT), 0);
+  const int nw = (T + 31) >> 5;
+  int base = 0;
+  for (int w0 = 0; w0 < nw; w0 += 256) {  // rounds of 256 bitmap words, in order
+    const int w = w0 + tid;
+    uint32_t word = w < nw ? bits[(size_t)e * wt + w] : 0u;
+    const int pos = base + block_exclusive_scan256(__popc(word), tmp);
+    int r = 0;
+    while (word) {
+      const int b = __ffs(word) - 1;
+      word &= word - 1u;
+      const int t = 32 * w + b;
+      int k = 0;
+      for (; k < K - 1; k++)
+        if (ids[(size_t)t * K + k] == e) break;
+      list[eoff + pos + r] = t * K + k;
+      r++;
+    }
+    if (tid == 255) tmp[4] = pos + r;  // round total (tmp[0..3] belong to the scan)
+    __syncthreads();
+    base = tmp[4];
+    __syncthreads();
   }
 }
 
