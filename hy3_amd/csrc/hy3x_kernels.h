@@ -53,8 +53,14 @@ extern template __global__ void k_down_gemv<1>(const uint8_t *, const __half *, 
 extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, const int32_t *,
                                                const int4 *, const int32_t *, float *);
 
+// Waves per workgroup of the MFMA grouped GEMMs: a tile has 16 MFMA_WAVES
+// gate/up rows (per matrix) or 32 MFMA_WAVES down rows.
+#ifndef HY3X_MFMA_WAVES
+#define HY3X_MFMA_WAVES 4
+#endif
+constexpr int MFMA_WAVES = HY3X_MFMA_WAVES;
 template <bool GATEUP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(
+__global__ __launch_bounds__(64 * MFMA_WAVES) void k_moe_mfma(
     const uint8_t *wq, const __half *act, const __half *act_sum, const int32_t *list,
     const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m, float *out);
 extern template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const __half *,

@@ -1,22 +1,42 @@
 // hy3x_mfma.hip -- grouped Q4_K x fp16 GEMMs on the matrix cores (prefill).
 //
-// A work tile is one expert, a slice of its weight matrix -- 64 rows of gate
-// and of up (four waves x 16 rows), or 128 rows of down (four waves x 2 x 16
-// rows) -- and up to 64 of its tokens (the dispatch tile list with NT = 64).
-// Per Q4_K block column (256 of K) every lane turns the 8-element runs of its
-// weight row that the MFMA needs into exact integers sc*q in fp16, straight
-// from the GGUF bytes (q via the 0x6400 exponent-bias trick, one packed fp16
-// FMA with the sub-block scale), while the block's activations for the column
-// sit in LDS. v_mfma_f32_16x16x32_f16 accumulates each block in fp32 (one MFMA
-// spans exactly one Q4_K sub-block of 32); d, dmin and the mins are applied
-// per block (see mfma_tile).
+// A work tile is one expert, a slice of its weight matrix -- 16 MFMA_WAVES
+// rows of gate and of up, or 32 MFMA_WAVES rows of down (each wave 16 or
+// 2 x 16 rows) -- and up to 32 of its tokens (the dispatch tile list with
+// NT = 32).
+//
+// Per Q4_K block column (256 of K):
+//  * the tile's 256 row-blocks (144 B each) are copied from HBM straight into
+//    LDS with coalesced 16-byte global->LDS loads (every row's block is 9
+//    consecutive chunks), through a ring of A_STAGES columns;
+//  * every lane turns 64 of its row's 256 weights into exact integers sc*q in
+//    fp16 (q via the 0x6400 exponent-bias trick, one packed fp16 FMA with the
+//    sub-block scale) -- the MFMA operands;
+//  * v_mfma_f32_16x16x32_f16 accumulates the block in fp32 against the
+//    tokens' activations (also copied global->LDS, double-buffered), then d,
+//    dmin and the mins are applied per block (see mfma_step).
+// All loads inside the column loop are these global->LDS copies, issued from
+// inline assembly: their completion is tracked by hand (s_waitcnt vmcnt on
+// the known number of copies in flight, then a barrier), which the compiler's
+// own wait insertion cannot do for LDS copies.
 //
 // Operand layouts (16x16x32): lane l holds A[l%16][8(l/16) .. +7] (row, k),
 // B[8(l/16) .. +7][l%16] (k, column) and D[4(l/16) + i][l%16], i = 0..3. Here
 // A = activations (rows = tokens) and B = weights (columns = weight rows), so
 // a lane's D values all belong to ONE weight row (its own: l%16) and four
-// tokens. Within each run of 8 the k order is (0,2,1,3,4,6,5,7), the order
-// the nibble unpack produces; activations are staged in that order (perm8).
+// tokens.
+//
+// k order inside a block: an MFMA only needs the A and B operands to agree on
+// which k each lane-slot carries, and the sub-block scales are folded into
+// the weights, so one MFMA may mix sub-blocks of one block. Lane group g
+// (= l/16) takes two contiguous 16-byte pieces of the block's 128 qs bytes,
+// [16g, 16g+16) and [64+16g, 64+16g+16) -- i.e. half (g&1) of qs chunks
+// p = g>>1 and p = 2 + (g>>1) -- and MFMA i = 4 piece + 2 h + u of the block
+// uses, from piece `piece`, bytes [8u, 8u+8): their low (h = 0) or high
+// (h = 1) nibbles, elements 16(g&1) + 8u .. +7 of sub-block 2p + h
+// (hy3.c:1030-1040). Within each run of 8 the element order is
+// (0,2,1,3,4,6,5,7), the order the nibble unpack produces; activations are
+// staged in that order (perm8).
 #include "hy3x_kernels.h"
 #include "hy3x_q4k.h"
 
@@ -26,10 +46,64 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));  // 16 bytes as a native vector
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int MT_TOK = 64;      // tokens per tile (dispatch NT)
-constexpr int BT_STRIDE = 264;  // fp16 per staged token row (256 + 8 pad: conflict-free reads)
-constexpr int BM_STRIDE = 40;   // fp16 per staged token mins row (32 + 8 pad)
+constexpr int MT_TOK = 32;                 // tokens per tile (dispatch NT for this path)
+constexpr int MT_WAVES = MFMA_WAVES;       // waves per workgroup
+constexpr int MT_THREADS = 64 * MT_WAVES;
+constexpr int RB = 32 * MT_WAVES;          // row-blocks per tile and block column
+constexpr int RB_HALF = 16 * MT_WAVES;     // gate/up: gate row-blocks, then up
+constexpr int RB_CHUNKS = 9;    // 16-byte chunks per row-block (144 B)
+constexpr int A_CHUNKS = RB * RB_CHUNKS;              // 2304 per column
+constexpr int A_CHUNKS_WAVE = A_CHUNKS / MT_WAVES;    // 288 per wave (32 row-blocks)
+constexpr int A_DMA = (A_CHUNKS_WAVE + 63) / 64;      // 5 copies per wave (last one half)
+#ifndef HY3X_A_STAGES
+#define HY3X_A_STAGES 2
+#endif
+constexpr int A_STAGES = HY3X_A_STAGES;               // weight ring stages
+constexpr int A_AHEAD = A_STAGES - 1;                 // weight columns copied ahead
+constexpr int B_DMA = MT_TOK * 32 / 64 / MT_WAVES;    // activation copies per wave
+constexpr int S_LANES = MT_TOK * 4 / MT_WAVES;        // lanes per wave copying sums
+// At the top of column kb's step, the weight copies of kb+1 .. kb+A_AHEAD-1
+// (issued last, A_DMA each) may still be in flight.
+constexpr int VM_IN_FLIGHT = (A_AHEAD - 1) * A_DMA;
+
+// LDS: the weight ring, the activations of a column (token rows of 32
+// 16-byte chunks, chunk c of row r at position c ^ (r & 15) so that the 16
+// rows an MFMA operand read touches hit 16 different bank groups) and their
+// sub-block sums (rows of 4 chunks, chunk p of row r at position
+// p ^ ((r >> 2) & 3)), both double-buffered, and the tile's slots.
+__shared__ __attribute__((aligned(16))) u4_t a_ring[A_STAGES][A_CHUNKS];
+__shared__ __attribute__((aligned(16))) u4_t bt_st[2][MT_TOK][32];
+__shared__ __attribute__((aligned(16))) u4_t bm_st[2][MT_TOK][4];
+__shared__ int32_t t_slot[MT_TOK], t_arow[MT_TOK];
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const lds_void_t *)p;
+}
+
+// 16-byte global -> LDS copy: lane i of the wave writes LDS bytes
+// [m0 + 16 i, m0 + 16 i + 16) (m0 = lds, wave-uniform). dma16_stream is the
+// weight copy; HY3X_WEIGHT_POLICY can add a cache-policy suffix to it (the
+// default caching measured best: a non-temporal " nt" was ~15% slower).
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+#ifndef HY3X_WEIGHT_POLICY
+#define HY3X_WEIGHT_POLICY ""
+#endif
+__device__ __forceinline__ void dma16_stream(const void *src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" HY3X_WEIGHT_POLICY ::"v"(src), "{m0}"(lds)
+               : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are in flight
+// and all its LDS operations are done, then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wait_copies_and_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 __device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, h2_t b, h2_t c) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(as_h2(a), b, c));
@@ -51,27 +125,23 @@ __device__ __forceinline__ Scales6 unpack_scales(const u4_t &h) {
   return r;
 }
 
-// fp16 pair (byte J0 of w, byte J1 of w) (values <= 63): the bytes go into the
-// mantissa of 1024.0, then 1024 is subtracted (both steps exact).
-template <int J0, int J1>
-__device__ __forceinline__ h2_t bytes_h2(uint32_t w) {
-  constexpr uint32_t sel = 0x0C000C00u | ((uint32_t)J1 << 16) | (uint32_t)J0;  // 0x0C: zero byte
+// fp16 pair of the two bytes of w that `sel` (a v_perm selector placing them
+// in bytes 0 and 2, zeros in 1 and 3) picks, values <= 63: the bytes go into
+// the mantissa of 1024.0, then 1024 is subtracted (both steps exact).
+__device__ __forceinline__ h2_t bytes_h2(uint32_t w, uint32_t sel) {
   const uint32_t v = __builtin_amdgcn_perm(w, w, sel) | 0x64006400u;
   return as_h2(v) + (h2_t){(_Float16)-1024.0f, (_Float16)-1024.0f};
 }
 
-// Weight operands of sub-blocks 2p (lo) and 2p+1 (hi) from the 8 bytes
-// qs[32p + 8g .. +7] of this lane's row: the exact integers sc*q in fp16
-// (sc*q <= 945). sc = (sc_lo, sc_hi). Low nibbles: 0x6400 | q = 1024 + q,
-// times sc_lo, minus 1024 sc_lo. High nibbles, left in place: 0x6400 | 16q =
-// 1024 + 16q, times sc_hi/16, minus 64 sc_hi. Each is one fused multiply-add
-// whose exact result is representable, so it is exact.
-__device__ __forceinline__ void dequant_pair(u2_t q, h2_t sc, h8_t &w_lo, h8_t &w_hi) {
+// Weight operands of one 8-byte run of qs: the low nibbles (sub-block scale
+// sc_lo) and the high nibbles (sc_hi) as exact integers sc*q in fp16
+// (sc*q <= 945). Low: 0x6400 | q = 1024 + q, times sc_lo, minus 1024 sc_lo.
+// High, left in place: 0x6400 | 16q = 1024 + 16q, times sc_hi/16, minus
+// 64 sc_hi. Each is one fused multiply-add whose exact result is
+// representable, so it is exact.
+__device__ __forceinline__ void dequant_run(u2_t q, h2_t ml, h2_t al, h2_t mh, h2_t ah,
+                                            h8_t &w_lo, h8_t &w_hi) {
   const uint32_t mag = 0x64006400u, m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
-  const h2_t mul = sc * (h2_t){(_Float16)1.0f, (_Float16)0.0625f};     // (sc_lo, sc_hi/16)
-  const h2_t add = sc * (h2_t){(_Float16)-1024.0f, (_Float16)-64.0f};  // (-1024 sc_lo, -64 sc_hi)
-  const h2_t ml = {mul[0], mul[0]}, al = {add[0], add[0]};
-  const h2_t mh = {mul[1], mul[1]}, ah = {add[1], add[1]};
   const uint32_t x8 = q.x >> 8, y8 = q.y >> 8;
   u4_t lo, hi;
   lo.x = pk_fma_f16(and_or(q.x, m_lo, mag), ml, al);
@@ -100,205 +170,241 @@ __device__ __forceinline__ h8_t mins_operand(float dmin, uint32_t m2) {
 
 template <bool GATEUP>
 struct MfmaCfg {
-  static constexpr int KD = GATEUP ? D : F;      // reduction length
-  static constexpr int NROWS = GATEUP ? F : D;   // weight rows
-  static constexpr int RG = GATEUP ? 1 : 2;      // 16-row groups per wave
-  static constexpr int TROWS = 64 * RG;          // weight rows per tile
-  static constexpr int NRT = NROWS / TROWS;      // row tiles
-  static constexpr int NKB = KD / QK;            // Q4_K block columns
-  static constexpr int NSUB = KD / 32;           // sub-blocks per activation row
-  static constexpr int NMAT = GATEUP ? 2 : 1;    // gate and up, or down
+  static constexpr int KD = GATEUP ? D : F;        // reduction length
+  static constexpr int NROWS = GATEUP ? F : D;     // weight rows
+  static constexpr int RG = GATEUP ? 1 : 2;        // 16-row groups per wave
+  static constexpr int TROWS = 16 * MT_WAVES * RG; // weight rows per tile
+  static constexpr int NRT = NROWS / TROWS;        // row tiles
+  static constexpr int NKB = KD / QK;              // Q4_K block columns (16 / 6)
+  static constexpr int NSUB = KD / 32;             // sub-blocks per activation row
+  static constexpr int NMAT = GATEUP ? 2 : 1;      // gate and up, or down
+  static_assert(TROWS * NMAT == RB, "row-blocks per tile");
 };
 
-struct MfmaSmem {
-  _Float16 bt[2][MT_TOK][BT_STRIDE];  // activations of one block column (double-buffered)
-  _Float16 bm[2][MT_TOK][BM_STRIDE];  // their sub-block sums as (Sh, Sl, Sh, Sl) per sub-block
-  int32_t slot[MT_TOK], arow[MT_TOK];
+// Per-thread copy sources of one work tile (column 0; column kb adds kb
+// blocks).
+template <bool GATEUP, int NTT>
+struct TileState {
+  using C = MfmaCfg<GATEUP>;
+  static constexpr int RG = C::RG, NMAT = C::NMAT;
+  const uint8_t *asrc[A_DMA];   // weight chunks
+  bool a_last;                  // the half-used last weight copy is active in this lane
+  const __half *bsrc[B_DMA];    // activation chunks
+  const __half *ssrc;           // sums chunk (lanes below S_LANES)
+  f4_t acc[RG][NMAT][NTT];
 };
 
-// One work tile with NTT token tiles of 16 (n <= 16 * NTT tokens).
-//
-// Per block column, for each (token tile, weight row group, matrix):
-//   Dblk = sum over the 8 sub-blocks of MFMA(x, sc*q)   (exact integer weights)
-//   acc = MFMA(S, -dmin*m, acc)                         (mins term)
-//   acc += d * Dblk                                     (fp32, d of the lane's row)
+// Copies of column kb: activations and sums into buffer kb & 1, then weights
+// of column ka into ring stage ka % 3 -- always B_DMA + 1 + A_DMA copies per
+// wave, weights last.
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void issue_b(const TileState<GATEUP, NTT> &st, int kb) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int buf = kb & 1;
+#pragma unroll
+  for (int j = 0; j < B_DMA; j++)
+    dma16(st.bsrc[j] + kb * QK,
+          __builtin_amdgcn_readfirstlane(lds_addr(&bt_st[buf][0][0] + 64 * (B_DMA * wave + j))));
+  if (lane < S_LANES)
+    dma16(st.ssrc + kb * 32,
+          __builtin_amdgcn_readfirstlane(lds_addr(&bm_st[buf][0][0] + S_LANES * wave)));
+}
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void issue_a(const TileState<GATEUP, NTT> &st, int ka) {
+  const int wave = threadIdx.x >> 6;
+  const u4_t *dst = &a_ring[ka % A_STAGES][0] + A_CHUNKS_WAVE * wave;
+#pragma unroll
+  for (int j = 0; j < A_DMA; j++)
+    if (j < A_DMA - 1 || st.a_last)
+      dma16_stream(st.asrc[j] + (size_t)ka * QB,
+                   __builtin_amdgcn_readfirstlane(lds_addr(dst + 64 * j)));
+}
+
+// One block column kb. Its copies were issued one (activations) and A_AHEAD
+// (weights) columns earlier; once they are in, the copies of kb + 1 and
+// kb + A_AHEAD are issued into the buffers column kb - 1 used, and kb is
+// computed.
+// Per (token tile, weight row group, matrix):
+//   Dblk = sum of the 8 MFMAs of the block (exact integer weights sc*q)
+//   acc  = MFMA(S, -dmin*m, acc) + d * Dblk      (d, dmin of the lane's row)
 // -- the Q4_K identity sum_k w_k x_k = d sum_j sc_j sum_{k in j} q_k x_k
 // - dmin sum_j m_j sum_{k in j} x_k (hy3.c:1036-1037).
-//
-// Pipeline: the weights (registers) and activations (registers, then the LDS
-// buffer of the next column) of column kb+1 are fetched while column kb runs;
-// one barrier per column.
 template <bool GATEUP, int NTT>
-__device__ __forceinline__ void mfma_tile(MfmaSmem &sm, const uint8_t *__restrict__ wq,
+__device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
+  using C = MfmaCfg<GATEUP>;
+  constexpr int RG = C::RG, NMAT = C::NMAT, NKB = C::NKB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, g = lane >> 4;
+  const int buf = kb & 1;
+  // this wave's copies of column kb have landed (only the weights of
+  // kb + 1 .. kb + A_AHEAD - 1, the last copies issued, may be in flight) and
+  // its reads of kb - 1 are done; after the barrier the same holds for every
+  // wave
+  wait_copies_and_barrier<VM_IN_FLIGHT>();
+  issue_b(st, kb + 1 < NKB ? kb + 1 : NKB - 1);  // past the end: a harmless re-copy
+  issue_a(st, kb + A_AHEAD < NKB ? kb + A_AHEAD : NKB - 1);
+
+  const u4_t *as = &a_ring[kb % A_STAGES][0];
+  // byte selector of this lane group's sub-block pairs, activation chunk offset
+  const uint32_t sel =
+      0x0C000C00u | ((uint32_t)(2 * (g >> 1) + 1) << 16) | (uint32_t)(2 * (g >> 1));
+  const int gch = 8 * (g >> 1) + 2 * (g & 1);  // chunk (8 fp16) of k offset 64(g>>1) + 16(g&1)
+  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  // All LDS reads of the column first (weights: header and two qs pieces per
+  // row-block; activations: 8 fragments per token tile; sums), so that their
+  // latency is covered by the dequantisation below, not paid per MFMA.
+  u4_t hdr[RG][NMAT], pv[RG][NMAT][2];
+#pragma unroll
+  for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+      const int rb = GATEUP ? m * RB_HALF + 16 * wave + lr : 16 * (2 * wave + rg) + lr;
+      hdr[rg][m] = as[rb * RB_CHUNKS];
+      pv[rg][m][0] = as[rb * RB_CHUNKS + 1 + g];
+      pv[rg][m][1] = as[rb * RB_CHUNKS + 5 + g];
+    }
+  h8_t x[NTT][8], sv[NTT];
+#pragma unroll
+  for (int t = 0; t < NTT; t++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      // MFMA i = 4 piece + 2 h + u: k0 = 128 piece + 32 h + 8 u + 64 (g>>1) + 16 (g&1)
+      const int c = 16 * (i >> 2) + 4 * ((i >> 1) & 1) + (i & 1) + gch;
+      x[t][i] = __builtin_bit_cast(h8_t, bt_st[buf][16 * t + lr][c ^ lr]);
+    }
+    sv[t] = __builtin_bit_cast(h8_t, bm_st[buf][16 * t + lr][g ^ ((lr >> 2) & 3)]);
+  }
+
+  f4_t dblk[RG][NMAT][NTT];
+#pragma unroll
+  for (int piece = 0; piece < 2; piece++) {
+    h8_t wf[RG][NMAT][4];  // [2h + u]
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+      for (int m = 0; m < NMAT; m++) {
+        const Scales6 s6 = unpack_scales(hdr[rg][m]);
+        const h2_t sc = bytes_h2(s6.sc[piece], sel);                         // (sc_lo, sc_hi)
+        const h2_t mul = sc * (h2_t){(_Float16)1.0f, (_Float16)0.0625f};     // (sc_lo, sc_hi/16)
+        const h2_t add = sc * (h2_t){(_Float16)-1024.0f, (_Float16)-64.0f};  // (-1024 sc_lo, -64 sc_hi)
+        const h2_t ml = {mul[0], mul[0]}, al = {add[0], add[0]};
+        const h2_t mh = {mul[1], mul[1]}, ah = {add[1], add[1]};
+        dequant_run(pv[rg][m][piece].xy, ml, al, mh, ah, wf[rg][m][0], wf[rg][m][2]);
+        dequant_run(pv[rg][m][piece].zw, ml, al, mh, ah, wf[rg][m][1], wf[rg][m][3]);
+      }
+#pragma unroll
+    for (int hu = 0; hu < 4; hu++) {  // 2h + u
+      const int i = 4 * piece + hu;
+#pragma unroll
+      for (int t = 0; t < NTT; t++)
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+          for (int m = 0; m < NMAT; m++)
+            dblk[rg][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                x[t][i], wf[rg][m][hu], i == 0 ? zero4 : dblk[rg][m][t], 0, 0, 0);
+    }
+  }
+  // per-block scale d (of this lane's row) and the mins MFMA
+#pragma unroll
+  for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+      const u4_t hd = hdr[rg][m];
+      const float d = fp16_quirk(hd.x & 0xffffu), dmin = fp16_quirk(hd.x >> 16);
+      const Scales6 s6 = unpack_scales(hd);
+      // m_{2g}, m_{2g+1}: bytes 2(g & 1), 2(g & 1) + 1 of mn[g >> 1]
+      const uint32_t mw = (g >> 1) ? s6.mn[1] : s6.mn[0];
+      const h8_t mo = mins_operand(dmin, (g & 1) ? (mw >> 16) : mw);
+#pragma unroll
+      for (int t = 0; t < NTT; t++) {
+        st.acc[rg][m][t] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(sv[t], mo, st.acc[rg][m][t], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          st.acc[rg][m][t][i] = __builtin_fmaf(d, dblk[rg][m][t][i], st.acc[rg][m][t][i]);
+      }
+    }
+}
+
+// One work tile with NTT token tiles of 16 (n <= 16 * NTT tokens).
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
                                           const __half *__restrict__ act,
                                           const __half *__restrict__ act_sum, int e, int n,
                                           int rt, __half *__restrict__ h16m,
                                           float *__restrict__ out) {
   using C = MfmaCfg<GATEUP>;
   constexpr int RG = C::RG, NMAT = C::NMAT, NKB = C::NKB, KD = C::KD;
-  constexpr int NTOK = 16 * NTT;
-  constexpr int BU = NTOK / 8;  // activation uint4 per thread: tokens (tid >> 5) + 8u
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, g = lane >> 4;
+  TileState<GATEUP, NTT> st;
 
-  const uint8_t *abase[RG][NMAT];
+  // weights: wave w copies chunks [288 w, 288 w + 288) of the column's
+  // (row-block c / 9, 16-byte piece c % 9), 64 per copy
+  const uint8_t *ebase = wq + (size_t)e * EXPERT_BYTES;
 #pragma unroll
-  for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-    for (int m = 0; m < NMAT; m++)
-      abase[rg][m] = wq + (size_t)e * EXPERT_BYTES + (size_t)(GATEUP ? m : 2) * MAT_BYTES +
-                     (size_t)(rt * C::TROWS + 16 * (wave * RG + rg) + lr) * NKB * QB;
-
-  // Activation staging: thread tid moves 16-byte chunk (tid & 31) of tokens
-  // (tid >> 5) + 8u, and threads below 4 * NTOK a quarter of one token's sums
-  // row. Token slots past n re-load token 0's row (their D rows are never
-  // stored), so every prefetch register is written unconditionally.
-  const int bc = tid & 31, bt0 = tid >> 5;
-  const int arow0 = sm.arow[0];
-  const u4_t *bsrc[BU];
-#pragma unroll
-  for (int u = 0; u < BU; u++) {
-    const int ar = sm.arow[bt0 + 8 * u];
-    bsrc[u] = reinterpret_cast<const u4_t *>(act + (size_t)(ar >= 0 ? ar : arow0) * KD) + bc;
+  for (int j = 0; j < A_DMA; j++) {
+    int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
+    if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
+    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
+    const int m = GATEUP ? rb / RB_HALF : 2, lrow = GATEUP ? rb % RB_HALF : rb;
+    st.asrc[j] = ebase + (size_t)m * MAT_BYTES + (size_t)(rt * C::TROWS + lrow) * NKB * QB + 16 * pc;
   }
-  const bool s_mover = tid < 4 * NTOK;
-  const int ars = s_mover ? sm.arow[tid >> 2] : -1;
-  const u4_t *ssrc =
-      reinterpret_cast<const u4_t *>(act_sum + (size_t)(ars >= 0 ? ars : arow0) * C::NSUB * 4) +
-      (tid & 3);
-
-  u4_t bnext[BU];
-  u4_t snext = {0u, 0u, 0u, 0u};
-  u4_t hnext[RG][NMAT];
-  u2_t qnext[RG][NMAT][4];
-  // fetch column 0
+  st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
+  // activations: copy j of wave w fills positions q = 64 (B_DMA w + j) + lane
+  // of the 32 x 32 chunk tile: row r = q / 32, position q % 32 holds chunk
+  // (q % 32) ^ (r & 15). Sums: lane (< S_LANES) of wave w fills position
+  // q = S_LANES w + lane of the 32 x 4 tile: row q / 4, position q % 4 holds
+  // part (q % 4) ^ ((row >> 2) & 3). Rows past n copy token 0's row (their D
+  // rows are never stored).
+  const int arow0 = t_arow[0];
 #pragma unroll
-  for (int u = 0; u < BU; u++) bnext[u] = bsrc[u][0];
-  if (s_mover) snext = ssrc[0];
-#pragma unroll
-  for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-    for (int m = 0; m < NMAT; m++) {
-      hnext[rg][m] = *reinterpret_cast<const u4_t *>(abase[rg][m]);
-#pragma unroll
-      for (int p = 0; p < 4; p++)
-        qnext[rg][m][p] = *reinterpret_cast<const u2_t *>(abase[rg][m] + 16 + 32 * p + 8 * g);
-    }
-
-  f4_t acc[RG][NMAT][NTT];
+  for (int j = 0; j < B_DMA; j++) {
+    const int q = 64 * (B_DMA * wave + j) + lane, r = q >> 5;
+    const int ar = t_arow[r] >= 0 ? t_arow[r] : arow0;
+    st.bsrc[j] = act + (size_t)ar * KD + 8 * ((q & 31) ^ (r & 15));
+  }
+  {
+    const int q = S_LANES * wave + (lane & (S_LANES - 1)), r = q >> 2;
+    const int ar = t_arow[r] >= 0 ? t_arow[r] : arow0;
+    st.ssrc = act_sum + (size_t)ar * C::NSUB * 4 + 8 * ((q & 3) ^ ((r >> 2) & 3));
+  }
   const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-      for (int t = 0; t < NTT; t++) acc[rg][m][t] = zero4;
+      for (int t = 0; t < NTT; t++) st.acc[rg][m][t] = zero4;
 
-  for (int kb = 0; kb < NKB; kb++) {
-    const int buf = kb & 1;
+  // prologue: weights of column 0, activations of column 0, weights of
+  // columns 1 .. A_AHEAD - 1
+  issue_a(st, 0);
+  issue_b(st, 0);
 #pragma unroll
-    for (int u = 0; u < BU; u++) *reinterpret_cast<u4_t *>(&sm.bt[buf][bt0 + 8 * u][8 * bc]) = bnext[u];
-    if (s_mover) *reinterpret_cast<u4_t *>(&sm.bm[buf][tid >> 2][8 * (tid & 3)]) = snext;
-    u4_t hdr[RG][NMAT];
-    u2_t qv[RG][NMAT][4];
-#pragma unroll
-    for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-      for (int m = 0; m < NMAT; m++) {
-        hdr[rg][m] = hnext[rg][m];
-#pragma unroll
-        for (int p = 0; p < 4; p++) qv[rg][m][p] = qnext[rg][m][p];
-      }
-    __syncthreads();  // buf is staged; buf ^ 1 is no longer read (column kb - 1 is done)
-    // fetch column kb + 1 (the last iteration re-fetches column kb: harmless, no branch)
-    const int kn = kb + 1 < NKB ? kb + 1 : kb;
-#pragma unroll
-    for (int u = 0; u < BU; u++) bnext[u] = bsrc[u][kn * (QK / 8)];
-    if (s_mover) snext = ssrc[kn * 4];
-#pragma unroll
-    for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-      for (int m = 0; m < NMAT; m++) {
-        const uint8_t *bp = abase[rg][m] + (size_t)kn * QB;
-        hnext[rg][m] = *reinterpret_cast<const u4_t *>(bp);
-#pragma unroll
-        for (int p = 0; p < 4; p++)
-          qnext[rg][m][p] = *reinterpret_cast<const u2_t *>(bp + 16 + 32 * p + 8 * g);
-      }
+  for (int c = 1; c < A_AHEAD; c++) issue_a(st, c < NKB ? c : NKB - 1);
+  for (int kb = 0; kb < NKB; kb++) mfma_step(st, kb);
+  // drain the trailing re-copies before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    Scales6 sc6[RG][NMAT];
-#pragma unroll
-    for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-      for (int m = 0; m < NMAT; m++) sc6[rg][m] = unpack_scales(hdr[rg][m]);
-    f4_t dblk[RG][NMAT][NTT];
-#pragma unroll
-    for (int p = 0; p < 4; p++) {  // sub-blocks 2p and 2p+1
-      h8_t wf[2][RG][NMAT];
-#pragma unroll
-      for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-          const uint32_t w = sc6[rg][m].sc[p >> 1];
-          const h2_t sc = (p & 1) ? bytes_h2<2, 3>(w) : bytes_h2<0, 1>(w);
-          dequant_pair(qv[rg][m][p], sc, wf[0][rg][m], wf[1][rg][m]);
-        }
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int sb = 2 * p + h;
-#pragma unroll
-        for (int t = 0; t < NTT; t++) {
-          const h8_t x =
-              *reinterpret_cast<const h8_t *>(&sm.bt[buf][16 * t + lr][32 * sb + 8 * g]);
-#pragma unroll
-          for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-            for (int m = 0; m < NMAT; m++)
-              dblk[rg][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                  x, wf[h][rg][m], sb == 0 ? zero4 : dblk[rg][m][t], 0, 0, 0);
-        }
-      }
-    }
-    // per-block scale d (of this lane's row) and the mins MFMA
-    h8_t sv[NTT];
-#pragma unroll
-    for (int t = 0; t < NTT; t++)
-      sv[t] = *reinterpret_cast<const h8_t *>(&sm.bm[buf][16 * t + lr][8 * g]);
-#pragma unroll
-    for (int rg = 0; rg < RG; rg++)
-#pragma unroll
-      for (int m = 0; m < NMAT; m++) {
-        const u4_t hd = hdr[rg][m];
-        const float d = fp16_quirk(hd.x & 0xffffu), dmin = fp16_quirk(hd.x >> 16);
-        // m_{2g}, m_{2g+1}: bytes 2(g & 1), 2(g & 1) + 1 of mn[g >> 1]
-        const uint32_t mw = (g >> 1) ? sc6[rg][m].mn[1] : sc6[rg][m].mn[0];
-        const h8_t mo = mins_operand(dmin, (g & 1) ? (mw >> 16) : mw);
-#pragma unroll
-        for (int t = 0; t < NTT; t++) {
-          acc[rg][m][t] =
-              __builtin_amdgcn_mfma_f32_16x16x32_f16(sv[t], mo, acc[rg][m][t], 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; i++)
-            acc[rg][m][t][i] = __builtin_fmaf(d, dblk[rg][m][t][i], acc[rg][m][t][i]);
-        }
-      }
-  }
   // epilogue: lane holds D[token 16t + 4g + i][row] for its own weight row
 #pragma unroll
   for (int rg = 0; rg < RG; rg++) {
-    const int r = rt * C::TROWS + 16 * (wave * RG + rg) + lr;
+    const int r = rt * C::TROWS + 16 * (GATEUP ? wave : 2 * wave + rg) + lr;
 #pragma unroll
     for (int t = 0; t < NTT; t++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int tok = 16 * t + 4 * g + i;
         if (tok < n) {
-          const int slot = sm.slot[tok];
+          const int slot = t_slot[tok];
           if constexpr (GATEUP) {
             h16m[(size_t)slot * F + perm8(r)] =
-                __float2half(silu(acc[rg][0][t][i]) * acc[rg][1][t][i]);
+                __float2half(silu(st.acc[rg][0][t][i]) * st.acc[rg][1][t][i]);
           } else {
-            out[(size_t)slot * D + r] = acc[rg][0][t][i];
+            out[(size_t)slot * D + r] = st.acc[rg][0][t][i];
           }
         }
       }
@@ -314,13 +420,13 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return x * q + (x < r ? x : r) + i;
 }
 
-// Grouped GEMM over the tile list. GATEUP: weights = gate and up rows of the
-// expert (K = 4096), activations = staged s, epilogue h = silu(g) * u ->
-// h16m[slot][perm8(row)] (fp16). Otherwise weights = down rows (K = 1536),
-// activations = h16m, out[slot][row] fp32. act_sum: sub-block sums of each
-// activation row as (Sh, Sl, Sh, Sl) fp16 quadruples.
+// Grouped GEMM over the tile list (tiles of at most 32 tokens). GATEUP:
+// weights = gate and up rows of the expert (K = 4096), activations = staged
+// s, epilogue h = silu(g) * u -> h16m[slot][perm8(row)] (fp16). Otherwise
+// weights = down rows (K = 1536), activations = h16m, out[slot][row] fp32.
+// act_sum: sub-block sums of each activation row as (Sh, Sl, Sh, Sl) fp16.
 template <bool GATEUP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_moe_mfma(
+__global__ __launch_bounds__(MT_THREADS) void k_moe_mfma(
     const uint8_t *__restrict__ wq, const __half *__restrict__ act,
     const __half *__restrict__ act_sum, const int32_t *__restrict__ list,
     const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles, int T, int K,
@@ -331,21 +437,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   if (tile >= *n_tiles) return;
   const int4 td = tiles[tile];
   const int e = td.x, o = td.y, n = td.z;
-  __shared__ __attribute__((aligned(16))) MfmaSmem sm;
   const int tid = threadIdx.x;
   if (tid < MT_TOK) {
     const int s = tid < n ? list[o + tid] : -1;
-    sm.slot[tid] = s;
+    t_slot[tid] = s;
     // activation row: gate/up reads s of the token, down reads h of the slot
-    sm.arow[tid] = s < 0 ? -1 : (GATEUP ? (s < T * K ? s / K : s - T * K) : s);
+    t_arow[tid] = s < 0 ? -1 : (GATEUP ? (s < T * K ? s / K : s - T * K) : s);
   }
   __syncthreads();
-  switch ((n + 15) >> 4) {
-    case 1: mfma_tile<GATEUP, 1>(sm, wq, act, act_sum, e, n, rt, h16m, out); break;
-    case 2: mfma_tile<GATEUP, 2>(sm, wq, act, act_sum, e, n, rt, h16m, out); break;
-    case 3: mfma_tile<GATEUP, 3>(sm, wq, act, act_sum, e, n, rt, h16m, out); break;
-    default: mfma_tile<GATEUP, 4>(sm, wq, act, act_sum, e, n, rt, h16m, out); break;
-  }
+  if (n > 16)
+    mfma_tile<GATEUP, 2>(wq, act, act_sum, e, n, rt, h16m, out);
+  else
+    mfma_tile<GATEUP, 1>(wq, act, act_sum, e, n, rt, h16m, out);
 }
 
 // Sub-block sums of one fp16 row of n32 * 32 values, as (Sh, Sl, Sh, Sl) with
