@@ -43,6 +43,9 @@ def parse():
     p.add_argument("--secondary", action="store_true", help="also measure the other configs")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--graph", action="store_true",
+                   help="replay a HIP graph of each step's kernels instead of launching them "
+                        "directly (measured slower than direct launches on ROCm 7.2)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB --steps times (the known-size "
                         "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -81,14 +84,25 @@ def default_steps(T, n_layers):
     return {1: 2000, 32: 500}.get(T, 50 if T <= 512 else 10)
 
 
-def stage_bytes(stage, U, T, K):
-    """Algorithmic HBM bytes of one launch of a kernel stage."""
+def stage_bytes(stage, U, T, K, decode):
+    """Algorithmic HBM bytes of one launch of a kernel stage. Single-token
+    decode: the router stage also streams the shared expert's gate/up and the
+    gate/up stage streams the K routed experts only."""
+    router = 192 * 4096 * 4 + 4096 * 4 + T * 4096 * 4 + T * 4096 * 6
+    if decode:
+        if stage == "gateup":
+            return K * 2 * MAT + 4096 * 2 + K * 1536 * 2
+        if stage == "down":
+            return (K + 1) * MAT + (K + 1) * 1536 * 2 + 2 * 4096 * 4
+        if stage == "router":
+            return router + 2 * MAT + 1536 * 2
+        return 0
     if stage == "gateup":
         return U * 2 * MAT + T * 4096 * 2 + T * (K + 1) * 1536 * 2
     if stage == "down":
         return U * MAT + T * (K + 1) * (1536 * 2 + 4096 * 4)
     if stage == "router":
-        return 192 * 4096 * 4 + 4096 * 4 + T * 4096 * 4 + T * 4096 * 6
+        return router
     return 0
 
 
@@ -102,7 +116,7 @@ def dominant_kernel(stage, T, path):
     return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
 
 
-def measure(torch, H, C, cfg, steps, warmup):
+def measure(torch, H, C, cfg, steps, warmup, use_graph=False):
     layers = []
     for li in range(cfg.n_layers):
         L = H.MoELayer(cfg.T)
@@ -113,9 +127,23 @@ def measure(torch, H, C, cfg, steps, warmup):
     x = torch.from_numpy(C.inputs(cfg.input_seed, cfg.T).copy()).cuda()
     stream = torch.cuda.current_stream().cuda_stream
 
-    def step():
+    def eager_step():
         for L in layers:
             L.forward(x.data_ptr(), cfg.T, cfg.K, stream=stream)
+
+    step = eager_step
+    if use_graph:
+        # one graph per step: every layer's kernels, replayed as one launch
+        eager_step()
+        torch.cuda.synchronize()
+        graph, side = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for L in layers:
+                    L.forward(x.data_ptr(), cfg.T, cfg.K, stream=side.cuda_stream)
+        torch.cuda.current_stream().wait_stream(side)
+        step = graph.replay
 
     for _ in range(warmup):
         step()
@@ -136,7 +164,7 @@ def measure(torch, H, C, cfg, steps, warmup):
     for L in layers:
         L.set_timing(True)
     for _ in range(steps):
-        step()
+        eager_step()
     torch.cuda.synchronize()
     stages = {}
     nfw = 0
@@ -149,7 +177,8 @@ def measure(torch, H, C, cfg, steps, warmup):
     stage_us = {k: v * 1e3 / max(nfw, 1) for k, v in stages.items()}
     dom = max(("gateup", "down"), key=lambda k: stage_us[k])
     kernel = dominant_kernel(dom, cfg.T, layers[0].path)
-    dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K)
+    decode = cfg.T == 1 and layers[0].path == 0
+    dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K, decode)
     # launch duration of the dominant kernel: replayed back to back on the launch
     # stream between two HIP events, after the timed forwards
     reps = max(10, min(steps, 2000))
@@ -220,7 +249,7 @@ def main():
     torch.cuda.init()
     cfg = C.CONFIGS[a.config]
     steps = a.steps or default_steps(cfg.T, cfg.n_layers)
-    r = measure(torch, H, C, cfg, steps, a.warmup)
+    r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph)
     out = {
         "metric": "MoE-layer tokens/s (decode B=1) and achieved HBM GB/s vs peak",
         "value": round(r["tokens_per_s"], 2),
@@ -232,7 +261,8 @@ def main():
         "data": "synthetic (seeded, BASELINE configs; random-init Q4_K weights)",
         "config": {"workload": f"config{cfg.index}:{cfg.name}", "tokens": cfg.T,
                    "layers": cfg.n_layers, "top_k": cfg.K, "experts": "192+1 shared",
-                   "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu"},
+                   "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu",
+                   "launch": "hip-graph" if a.graph else "direct"},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),
                   "hbm_frac": round(r["layer_GBps"] / PEAK_HBM_GBS, 4),
                   "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},
@@ -243,7 +273,8 @@ def main():
         for c in C.CONFIGS:
             if c.index == cfg.index:
                 continue
-            rr = measure(torch, H, C, c, default_steps(c.T, c.n_layers), 3)
+            rr = measure(torch, H, C, c, default_steps(c.T, c.n_layers), 3,
+                         use_graph=a.graph)
             sec[f"config{c.index}:{c.name}"] = {
                 "tokens_per_s": round(rr["tokens_per_s"], 1),
                 "ms_per_step": round(rr["ms_per_step"], 4),

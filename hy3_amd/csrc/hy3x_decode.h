@@ -1,0 +1,106 @@
+// hy3x_decode.h -- single-token (decode) expert row streaming shared by the
+// routing kernel (shared expert) and the routed gate/up kernel.
+#pragma once
+#include "hy3x_q4k.h"
+
+namespace hy3x {
+
+// Gate and up rows r0 .. r0 + RPW - 1 of expert e for one token: each lane
+// owns one 64-weight group of the row (lane = 4 * block + pair), X holds the
+// token's staged s for that group and slo/shi its sub-block sums. The rows'
+// Q4_K bytes go through a ring of PF rows in flight; the wave reduces each
+// row dot with DPP and lane 0 writes h = silu(g) * u, pair-staged, to
+// h16[slot * F + ...] (hy3.c:1296-1300 / 1307-1314).
+template <int RPW, int PF>
+__device__ __forceinline__ void gateup_rows(const uint8_t *__restrict__ wq, int e, int slot,
+                                            int r0, const uint32_t (&X)[32], float slo,
+                                            float shi, __half *__restrict__ h16) {
+  const int lane = threadIdx.x & 63, b = lane >> 2, p = lane & 3;
+  const ScaleSel sel(p);
+  const uint8_t *gbase = wq + (size_t)e * EXPERT_BYTES + (size_t)b * QB;
+  const uint8_t *ubase = gbase + MAT_BYTES;
+  uint4 ring[PF][6];
+  auto issue = [&](int rr, uint4 (&dst)[6]) {
+    const uint8_t *gp = gbase + (size_t)(r0 + rr) * (D / QK) * QB;
+    const uint8_t *up = ubase + (size_t)(r0 + rr) * (D / QK) * QB;
+    dst[0] = *reinterpret_cast<const uint4 *>(gp);
+    dst[1] = *reinterpret_cast<const uint4 *>(gp + 16 + 32 * p);
+    dst[2] = *reinterpret_cast<const uint4 *>(gp + 32 + 32 * p);
+    dst[3] = *reinterpret_cast<const uint4 *>(up);
+    dst[4] = *reinterpret_cast<const uint4 *>(up + 16 + 32 * p);
+    dst[5] = *reinterpret_cast<const uint4 *>(up + 32 + 32 * p);
+  };
+#pragma unroll
+  for (int rr = 0; rr < PF && rr < RPW; rr++) issue(rr, ring[rr]);
+#pragma unroll
+  for (int rr = 0; rr < RPW; rr++) {
+    uint4 cur[6];
+#pragma unroll
+    for (int q = 0; q < 6; q++) cur[q] = ring[rr % PF][q];
+    if (rr + PF < RPW) issue(rr + PF, ring[rr % PF]);
+    uint32_t P[32];
+    unpack_group(cur[1], cur[2], P);
+    const float gv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
+    unpack_group(cur[4], cur[5], P);
+    const float uv = group_dot(P, X, slo, shi, block_scale(cur[3], sel));
+    const float g = wave_total(gv), u = wave_total(uv);
+    if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
+  }
+}
+
+// Down rows r0 .. r0 + 2 PASSES - 1 of expert e for one token, one wave:
+// each 32-lane half takes one row per pass (lane = one 64-weight group of
+// the 1536, 24 of the 32 lanes active), the passes' Q4_K go through a ring of
+// PF passes in flight, and fn(ps, sums) gets the two row sums of pass ps
+// (row r0 + 2 ps in .x, r0 + 2 ps + 1 in .y, wave-uniform). h: the slot's
+// staged h (hy3.c:1316-1317).
+template <int PASSES, int PF, typename Fn>
+__device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
+                                          const __half *__restrict__ h, int r0, Fn &&fn) {
+  constexpr int G = F / 64;
+  const int lane = threadIdx.x & 63, hw = lane >> 5, gl = lane & 31;
+  const bool active = gl < G;
+  const int b = gl >> 2, p = gl & 3;
+  const ScaleSel sel(p);
+  const uint8_t *dbase = wq + (size_t)e * EXPERT_BYTES + 2 * MAT_BYTES + (size_t)b * QB;
+  uint4 ring[PF][3];
+  auto issue = [&](int ps, uint4 (&dst)[3]) {
+    if (active) {
+      const uint8_t *dp = dbase + (size_t)(r0 + 2 * ps + hw) * (F / QK) * QB;
+      dst[0] = *reinterpret_cast<const uint4 *>(dp);
+      dst[1] = *reinterpret_cast<const uint4 *>(dp + 16 + 32 * p);
+      dst[2] = *reinterpret_cast<const uint4 *>(dp + 32 + 32 * p);
+    }
+  };
+  // h first: loads complete in issue order for the wait counters, so h
+  // issued after the weight ring would hold the first pass back until the
+  // whole ring had landed
+  uint32_t X[32];
+  if (active) load_group_x(h, gl, X);
+#pragma unroll
+  for (int ps = 0; ps < PF && ps < PASSES; ps++) issue(ps, ring[ps]);
+  float slo = 0.0f, shi = 0.0f;
+  if (active) group_sums(X, slo, shi);
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ps++) {
+    uint4 cur[3];
+#pragma unroll
+    for (int q = 0; q < 3; q++) cur[q] = ring[ps % PF][q];
+    if (ps + PF < PASSES) issue(ps + PF, ring[ps % PF]);
+    float dv = 0.0f;
+    if (active) {
+      uint32_t P[32];
+      unpack_group(cur[1], cur[2], P);
+      dv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
+    }
+    fn(ps, half_totals(dv));
+  }
+}
+
+// Decode launch shapes.
+constexpr int DEC_RPW = 4;                   // gate/up rows per wave
+constexpr int DEC_RPB = 4 * DEC_RPW;         // gate/up rows per block (four waves)
+constexpr int DEC_GU_BLOCKS = F / DEC_RPB;   // gate/up blocks per expert (96)
+constexpr int DEC_DOWN_RPB = 16;             // down rows per block
+
+}  // namespace hy3x

@@ -9,6 +9,7 @@
 // / moe_combine_id_kernel / add_kernel (hy3_gpu.cu:96-130, 140-142, 461-463)
 // and the CPU loops hy3.c:1293-1325.
 #include "hy3x_q4k.h"
+#include "hy3x_decode.h"
 #include "hy3x_route.h"
 
 namespace hy3x {
@@ -153,146 +154,72 @@ __global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ w
 // Decode fast path (T = 1): no dispatch. Slot k < K is routed expert ids[k],
 // slot K the shared expert; the expert id is one load away from the weights.
 
-// gate/up + SwiGLU. A block is 4 waves x 8 rows = 32 rows of one expert.
-// Blocks 0..47 are the shared expert (no routing needed, so they stream from
-// the first cycle); block 48(k+1) + c is routed slot k, whose first wave
-// routes the token from the 192 sigmoid values / scores (the routing
-// contract, identical in every block) before the weight loads start; block
-// 48 also publishes the routing. Weights stream through a 4-row prefetch ring.
+// Routed gate/up of a single token: block = 16 rows (four waves x 4) of
+// routed slot blockIdx.x / 96. Every block routes the token itself from the
+// 192 sigmoid values / scores (the routing contract, identical in every
+// block: topk_block) and takes expert sids[slot]; block 0 publishes the
+// routing and the stats. 768 blocks at 3 per CU: all resident at once.
 __global__ __launch_bounds__(256) void k_gateup_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ s16,
-    const float *__restrict__ sig, const float *__restrict__ score, int K,
-    float scale, int32_t *__restrict__ ids, float *__restrict__ wpre, float *__restrict__ wout,
+    const float *__restrict__ sig, const float *__restrict__ score, int K, float scale,
+    int32_t *__restrict__ ids, float *__restrict__ wpre, float *__restrict__ wout,
     unsigned long long *__restrict__ stats, __half *__restrict__ h16,
     unsigned long long *trace) {
-  constexpr int RPWAVE = 8, RPB = 32, CH = F / RPB, PF = 4;
-  const int sidx = blockIdx.x / CH, rc = blockIdx.x % CH;
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int b = lane >> 2, p = lane & 3;
-  uint32_t X[32];  // the token's staged s: independent of the routing, load it first
-  load_group_x(s16, lane, X);
-  int slot, e;
-  if (sidx == 0) {
-    slot = K;
-    e = E;
-  } else {
-    __shared__ int32_t sids[KMAX], scratch_l[4 * E + 2 * KMAX + 2];
-    __shared__ __attribute__((aligned(16))) float swp[KMAX], sw[KMAX], sc_l[E], sg_l[E];
-    topk_block(sig, score, K, scale, sids, swp, sw, sc_l, sg_l, scratch_l);
-    slot = sidx - 1;
-    e = sids[slot];
-    if (blockIdx.x == CH) {
-      if (threadIdx.x < K) {
-        ids[threadIdx.x] = sids[threadIdx.x];
-        wpre[threadIdx.x] = swp[threadIdx.x];
-        wout[threadIdx.x] = sw[threadIdx.x];
-      }
-      if (threadIdx.x == 0 && stats) {
-        stats[0] += 1ull;
-        stats[1] += (unsigned long long)(K + 1);
-      }
+  const int slot = blockIdx.x / DEC_GU_BLOCKS, rc = blockIdx.x % DEC_GU_BLOCKS;
+  // the token's staged s, once per block (the four waves read it from LDS)
+  __shared__ __attribute__((aligned(16))) __half s_l[D];
+  reinterpret_cast<uint4 *>(s_l)[threadIdx.x] = reinterpret_cast<const uint4 *>(s16)[threadIdx.x];
+  reinterpret_cast<uint4 *>(s_l)[threadIdx.x + 256] =
+      reinterpret_cast<const uint4 *>(s16)[threadIdx.x + 256];
+  __shared__ int32_t sids[KMAX], scratch_l[4 * E + 2 * KMAX + 2];
+  __shared__ __attribute__((aligned(16))) float swp[KMAX], sw[KMAX], sc_l[E], sg_l[E];
+  topk_block(sig, score, K, scale, sids, swp, sw, sc_l, sg_l, scratch_l);  // has barriers
+  trace_point(trace, 1);
+  uint32_t X[32];
+  load_group_x(s_l, lane, X);
+  const int e = sids[slot];
+  if (blockIdx.x == 0) {
+    if (threadIdx.x < K) {
+      ids[threadIdx.x] = sids[threadIdx.x];
+      wpre[threadIdx.x] = swp[threadIdx.x];
+      wout[threadIdx.x] = sw[threadIdx.x];
+    }
+    if (threadIdx.x == 0 && stats) {  // forwards, experts touched (shared included)
+      stats[0] += 1ull;
+      stats[1] += (unsigned long long)(K + 1);
     }
   }
-  trace_point(trace, 1);
-  const ScaleSel sel(p);
-  const uint8_t *gbase = wq + (size_t)e * EXPERT_BYTES + (size_t)b * QB;
-  const uint8_t *ubase = gbase + MAT_BYTES;
-  const int r0 = rc * RPB + wave * RPWAVE;
-  uint4 ring[PF][6];
-  auto issue = [&](int rr, uint4 (&dst)[6]) {
-    const uint8_t *gp = gbase + (size_t)(r0 + rr) * (D / QK) * QB;
-    const uint8_t *up = ubase + (size_t)(r0 + rr) * (D / QK) * QB;
-    dst[0] = *reinterpret_cast<const uint4 *>(gp);
-    dst[1] = *reinterpret_cast<const uint4 *>(gp + 16 + 32 * p);
-    dst[2] = *reinterpret_cast<const uint4 *>(gp + 32 + 32 * p);
-    dst[3] = *reinterpret_cast<const uint4 *>(up);
-    dst[4] = *reinterpret_cast<const uint4 *>(up + 16 + 32 * p);
-    dst[5] = *reinterpret_cast<const uint4 *>(up + 32 + 32 * p);
-  };
-#pragma unroll
-  for (int rr = 0; rr < PF; rr++) issue(rr, ring[rr]);
   float slo, shi;
   group_sums(X, slo, shi);
-  trace_point(trace, 2);
-#pragma unroll
-  for (int rr = 0; rr < RPWAVE; rr++) {
-    uint4 cur[6];
-#pragma unroll
-    for (int q = 0; q < 6; q++) cur[q] = ring[rr % PF][q];
-    if (rr + PF < RPWAVE) issue(rr + PF, ring[rr % PF]);
-    uint32_t P[32];
-    unpack_group(cur[1], cur[2], P);
-    const float gv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
-    unpack_group(cur[4], cur[5], P);
-    const float uv = group_dot(P, X, slo, shi, block_scale(cur[3], sel));
-    const float g = wave_total(gv), u = wave_total(uv);
-    if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
-  }
+  gateup_rows<DEC_RPW, DEC_RPW>(wq, e, slot, rc * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
   trace_point(trace, 3);
 }
 
-// down for all K+1 slots of rows blockIdx.x*16 .. +16, fused with the
-// combine y = x + (shared + sum_k w_k * down_k), k in selection order. Wave k
-// of the block (k = 0..K-1 routed slot k, k = K the shared expert) owns one
-// expert: its staged h group sits in registers (lane = group, 24 of each
-// 32-lane half), it streams the 16 rows' Q4_K through a 4-pass prefetch ring
-// (2 rows per pass) and leaves the row sums in LDS; 16 threads combine.
-__global__ __launch_bounds__(576) void k_down_decode(const uint8_t *__restrict__ wq,
-                                                     const __half *__restrict__ h16,
-                                                     const int32_t *__restrict__ ids,
-                                                     const float *__restrict__ w, int K,
-                                                     float *__restrict__ x,
-                                                     unsigned long long *trace) {
-  constexpr int G = F / 64, RPB = 16, PASSES = RPB / 2, PF = 4;
+// Down of a single token for rows blockIdx.x*16 .. +16, fused with the
+// combine y = x + (shared + sum_k w_k * down_k), k in selection order
+// (hy3.c:1302, 1318-1319, 1324-1325). Wave k owns slot k (k < K routed,
+// k = K the shared expert): its 8 passes of 2 rows stream through a ring of
+// 4 (down_rows; deeper rings measured slower), the row sums go to LDS, and 16
+// threads combine them.
+__global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
+    const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
+    const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
+    float *__restrict__ x, unsigned long long *trace) {
+  constexpr int RPB = DEC_DOWN_RPB;
   __shared__ float out_l[KMAX + 1][RPB];
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int hw = lane >> 5, gl = lane & 31;
-  const bool active = gl < G && k <= K;
-  const int b = gl >> 2, p = gl & 3;
   const int r0 = blockIdx.x * RPB;
-  if (k <= K) {
-    const int e = k < K ? ids[k] : E;
-    const ScaleSel sel(p);
-    const uint8_t *dbase = wq + (size_t)e * EXPERT_BYTES + 2 * MAT_BYTES + (size_t)b * QB;
-    uint4 ring[PF][3];
-    auto issue = [&](int ps, uint4 (&dst)[3]) {
-      if (active) {
-        const uint8_t *dp = dbase + (size_t)(r0 + 2 * ps + hw) * (F / QK) * QB;
-        dst[0] = *reinterpret_cast<const uint4 *>(dp);
-        dst[1] = *reinterpret_cast<const uint4 *>(dp + 16 + 32 * p);
-        dst[2] = *reinterpret_cast<const uint4 *>(dp + 32 + 32 * p);
-      }
-    };
-#pragma unroll
-    for (int ps = 0; ps < PF; ps++) issue(ps, ring[ps]);
-    uint32_t X[32];
-    float slo = 0.0f, shi = 0.0f;
-    if (active) {
-      load_group_x(h16 + (size_t)k * F, gl, X);
-      group_sums(X, slo, shi);
-    }
-    trace_point(trace, 1);
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ps++) {
-      uint4 cur[3];
-#pragma unroll
-      for (int q = 0; q < 3; q++) cur[q] = ring[ps % PF][q];
-      if (ps + PF < PASSES) issue(ps + PF, ring[ps % PF]);
-      float dv = 0.0f;
-      if (active) {
-        uint32_t P[32];
-        unpack_group(cur[1], cur[2], P);
-        dv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
-      }
-      const float2 tot = half_totals(dv);
-      if (lane == 0) {
-        out_l[k][2 * ps] = tot.x;
-        out_l[k][2 * ps + 1] = tot.y;
-      }
-    }
-  }
+  if (k <= K)
+    down_rows<RPB / 2, 4>(wq, k < K ? ids[k] : E, h16 + (size_t)k * F, r0,
+                          [&](int ps, float2 t) {
+                            if (lane == 0) {
+                              out_l[k][2 * ps] = t.x;
+                              out_l[k][2 * ps + 1] = t.y;
+                            }
+                          });
   __syncthreads();
   trace_point(trace, 2);
   if (threadIdx.x < RPB) {

@@ -38,6 +38,10 @@ __global__ void k_gateup_decode(const uint8_t *wq, const __half *s16, const floa
                                 const float *score, int K, float scale, int32_t *ids,
                                 float *wpre, float *wout, unsigned long long *stats,
                                 __half *h16, unsigned long long *trace);
+__global__ void k_route_decode(const float *x, const float *norm_w, const float *router,
+                               const float *bias, int has_bias, int K, float *logits,
+                               float *sig, float *score, __half *s16, float *s32,
+                               const uint8_t *wq, __half *h16, unsigned long long *trace);
 __global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *ids,
                               const float *w, int K, float *x, unsigned long long *trace);
 __global__ void k_combine(float *x, const float *out, const float *w, int T, int K);

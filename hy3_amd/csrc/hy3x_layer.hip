@@ -17,6 +17,7 @@
 
 #include "../../include/hy3x_moe.h"
 #include "hy3x_kernels.h"
+#include "hy3x_decode.h"
 
 using namespace hy3x;
 
@@ -235,6 +236,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
   float *x = c.x;
   switch (stage) {
     case HY3X_STAGE_ROUTER:
+      if (c.mode == Mode::DECODE) {
+        k_route_decode<<<E + DEC_GU_BLOCKS, 256, 0, st>>>(
+            x, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
+            L->s16, L->s32, L->wq, L->h16, L->trace[0]);
+        break;
+      }
       if (T <= kSmallRouterT) {
         k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias,
                                                     L->has_bias, L->logits, L->sig, L->score,
@@ -251,9 +258,8 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
           k_router_gemm<8, 4, 4, 8><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
       }
-      if (c.mode != Mode::DECODE)
-        k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, L->ids, L->wpre,
-                                  L->w);
+      k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, L->ids, L->wpre,
+                                L->w);
       break;
     case HY3X_STAGE_DISPATCH:
       if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);
@@ -269,9 +275,9 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_GATEUP:
       if (c.mode == Mode::DECODE)
-        k_gateup_decode<<<(K + 1) * (F / 32), 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
-                                                            c.scale, L->ids, L->wpre, L->w,
-                                                            L->stats, L->h16, L->trace[1]);
+        k_gateup_decode<<<K * DEC_GU_BLOCKS, 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
+                                                          c.scale, L->ids, L->wpre, L->w,
+                                                          L->stats, L->h16, L->trace[1]);
       else if (c.mode == Mode::MFMA)
         k_moe_mfma<true><<<mt * (F / (16 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->s16m, L->ssum, L->list,
                                                         L->tiles, L->n_tiles, T, K, L->h16m,
@@ -282,7 +288,8 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
-        k_down_decode<<<D / 16, 576, 0, st>>>(L->wq, L->h16, L->ids, L->w, K, x, L->trace[2]);
+        k_down_decode<<<D / DEC_DOWN_RPB, 64 * (KMAX + 1), 0, st>>>(L->wq, L->h16, L->ids, L->w,
+                                                                    K, x, L->trace[2]);
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
         k_moe_mfma<false><<<mt * (D / (32 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->h16m, L->hsum, L->list,

@@ -21,6 +21,7 @@
 // -fhip-fp32-correctly-rounded-divide-sqrt) and nothing in this file is
 // contracted into FMAs beyond the explicit fmaf calls.
 #include "hy3x_route.h"
+#include "hy3x_decode.h"
 
 #pragma clang fp contract(off)
 
@@ -62,19 +63,17 @@ __device__ __forceinline__ float chain_dot(const float *a, const float *b) {
 }
 
 // ---------------------------------------------------------------------------
-// Small T (decode): grid (192, T), one wave per (expert, token). The wave
-// stages x, norm_w and the router row in LDS transposed by chain
-// (buf[v][i] = a[8i+v]), lanes 0..7 run the eight sum-of-squares chains, then
-// the eight logit chains. The last block of a token (atomic ticket) runs the
-// top-K and resets the ticket, so the kernel can be relaunched or replayed
-// without clearing memory. Block (0, t) also stages s for the expert kernels.
-__global__ __launch_bounds__(256) void k_router_logits(
-    const float *__restrict__ x, const float *__restrict__ norm_w,
+// Small T: one block per (expert, token). The block stages x, norm_w and the
+// router row in LDS transposed by chain (buf[v][i] = a[8i+v]), reduces the
+// sum of squares in the fixed block order, then lanes 0..7 run the eight
+// logit chains. Block (0, t) also stages s for the expert kernels.
+__device__ __forceinline__ void router_block(
+    int e, int t, const float *__restrict__ x, const float *__restrict__ norm_w,
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
     __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace) {
   __shared__ __attribute__((aligned(16))) float xsf[8 * RS], wsf[8 * RS], rsf[8 * RS];
-  const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  const int tid = threadIdx.x;
   trace_point(trace, 0);
   float r_blk;
   {  // every load in flight at once: 4 float4 of each row per thread
@@ -122,6 +121,64 @@ __global__ __launch_bounds__(256) void k_router_logits(
       s32[(size_t)t * D + j] = sv;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void k_router_logits(
+    const float *__restrict__ x, const float *__restrict__ norm_w,
+    const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
+    float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
+    __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace) {
+  router_block(blockIdx.x, blockIdx.y, x, norm_w, router, bias, has_bias, logits, sig, score, s16,
+               s32, trace);
+}
+
+// Single token: router logits and the shared expert's gate/up in one launch.
+// Blocks 0..191 compute router logit e (router_block; block 0 also stages s).
+// Blocks 192.. need no routing: they compute s themselves (the same RMSNorm
+// arithmetic as router_block) and stream the shared expert's gate/up rows,
+// 16 per block, into h16 slot K. The top-K runs in the routed gate/up blocks
+// (k_gateup_decode): publishing it from here would need a device-scope
+// release/acquire between blocks, which costs more than recomputing it.
+__global__ __launch_bounds__(256) void k_route_decode(
+    const float *__restrict__ x, const float *__restrict__ norm_w,
+    const float *__restrict__ router, const float *__restrict__ bias, int has_bias, int K,
+    float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
+    __half *__restrict__ s16, float *__restrict__ s32, const uint8_t *__restrict__ wq,
+    __half *__restrict__ h16, unsigned long long *trace) {
+  const int tid = threadIdx.x;
+  if (blockIdx.x < E) {
+    router_block(blockIdx.x, 0, x, norm_w, router, bias, has_bias, logits, sig, score, s16, s32,
+                 trace);
+    return;
+  }
+  // shared expert: s = rmsnorm(x) * norm_w, pair-staged fp16 in LDS
+  trace_point(trace, 0);
+  __shared__ __attribute__((aligned(16))) __half s_l[D];
+  __shared__ float red_l[4];
+  const float4 *xg = reinterpret_cast<const float4 *>(x);
+  const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
+  float4 a[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) a[u] = xg[tid + 256 * u];
+  const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const float4 w = wg[tid + 256 * u];
+    const int j = 4 * (tid + 256 * u);
+    stage_store(s_l, j + 0, (a[u].x * w.x) * r);
+    stage_store(s_l, j + 1, (a[u].y * w.y) * r);
+    stage_store(s_l, j + 2, (a[u].z * w.z) * r);
+    stage_store(s_l, j + 3, (a[u].w * w.w) * r);
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6, sb = blockIdx.x - E;
+  uint32_t X[32];
+  load_group_x(s_l, lane, X);
+  float slo, shi;
+  group_sums(X, slo, shi);
+  trace_point(trace, 1);
+  gateup_rows<DEC_RPW, DEC_RPW>(wq, E, K, sb * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
+  trace_point(trace, 3);
 }
 
 // ---------------------------------------------------------------------------

@@ -296,3 +296,34 @@ def test_expert_paths_match_oracle(torch, layer, cpu, T):
             assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL, path
     finally:
         layer.set_path(0)
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_graph_replay_matches_eager(torch, layer, T):
+    """The forward only enqueues kernels, so it can be captured in a HIP graph
+    (as the engine captures its decode step). Every replay -- with eager work
+    and other forwards on the same layer in between -- reproduces the eager
+    result bit for bit."""
+    x0 = torch.from_numpy(C.inputs(0xC2, T).copy()).cuda()
+    xe = x0.clone()
+    layer.forward(xe.data_ptr(), T, 8)
+    torch.cuda.synchronize()
+    y_eager = xe.cpu().numpy()
+    xs = x0.clone()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            layer.forward(xs.data_ptr(), T, 8, stream=side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    other = torch.from_numpy(C.inputs(0xC1, T).copy()).cuda()
+    for rep in range(4):
+        xs.copy_(x0)
+        _ = (other @ other.T).sum()  # unrelated eager work
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(xs.cpu().numpy().view(np.uint32), y_eager.view(np.uint32)), rep
+        ot = other.clone()  # an eager forward on another buffer between replays
+        layer.forward(ot.data_ptr(), T, 8)
+        torch.cuda.synchronize()
