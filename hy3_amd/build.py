@@ -10,6 +10,8 @@ hy3_amd/libhy3x.so. Flags:
                                             no packed-fp32 instructions are
                                             generated (they are unreliable on
                                             the target machines).
+HY3X_EXTRA_FLAGS (environment) appends flags, e.g. the tile-shape macros of
+hy3x_mfma.hip for tuning runs.
 """
 import os
 import subprocess
@@ -28,7 +30,7 @@ FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-]
+] + os.environ.get("HY3X_EXTRA_FLAGS", "").split()  # e.g. "-DHY3X_MFMA_WAVES=8" (tuning runs)
 
 
 def sources():
