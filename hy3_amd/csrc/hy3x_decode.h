@@ -98,9 +98,20 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
 }
 
 // Decode launch shapes.
+#ifndef HY3X_GU_PF
+#define HY3X_GU_PF 4
+#endif
 constexpr int DEC_RPW = 4;                   // gate/up rows per wave
+constexpr int DEC_GU_PF = HY3X_GU_PF;        // gate/up rows in flight per wave
 constexpr int DEC_RPB = 4 * DEC_RPW;         // gate/up rows per block (four waves)
 constexpr int DEC_GU_BLOCKS = F / DEC_RPB;   // gate/up blocks per expert (96)
-constexpr int DEC_DOWN_RPB = 16;             // down rows per block
+#ifndef HY3X_DOWN_RPB
+#define HY3X_DOWN_RPB 16
+#endif
+#ifndef HY3X_DOWN_PF
+#define HY3X_DOWN_PF 2
+#endif
+constexpr int DEC_DOWN_RPB = HY3X_DOWN_RPB;  // down rows per block
+constexpr int DEC_DOWN_PF = HY3X_DOWN_PF;    // down passes (2 rows each) in flight per wave
 
 }  // namespace hy3x

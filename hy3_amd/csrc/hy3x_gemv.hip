@@ -193,16 +193,16 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
   }
   float slo, shi;
   group_sums(X, slo, shi);
-  gateup_rows<DEC_RPW, DEC_RPW>(wq, e, slot, rc * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
+  gateup_rows<DEC_RPW, DEC_GU_PF>(wq, e, slot, rc * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
   trace_point(trace, 3);
 }
 
-// Down of a single token for rows blockIdx.x*16 .. +16, fused with the
+// Down of a single token for rows blockIdx.x*RPB .. +RPB, fused with the
 // combine y = x + (shared + sum_k w_k * down_k), k in selection order
 // (hy3.c:1302, 1318-1319, 1324-1325). Wave k owns slot k (k < K routed,
-// k = K the shared expert): its 8 passes of 2 rows stream through a ring of
-// 4 (down_rows; deeper rings measured slower), the row sums go to LDS, and 16
-// threads combine them.
+// k = K the shared expert): its passes of 2 rows stream through a ring of
+// DEC_DOWN_PF (down_rows; 2 measured best: deeper rings were slower), the row sums go to
+// LDS, and DEC_DOWN_RPB threads combine them.
 __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
     const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
   const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int r0 = blockIdx.x * RPB;
   if (k <= K)
-    down_rows<RPB / 2, 4>(wq, k < K ? ids[k] : E, h16 + (size_t)k * F, r0,
+    down_rows<RPB / 2, DEC_DOWN_PF>(wq, k < K ? ids[k] : E, h16 + (size_t)k * F, r0,
                           [&](int ps, float2 t) {
                             if (lane == 0) {
                               out_l[k][2 * ps] = t.x;
