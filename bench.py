@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--secondary", action="store_true", help="also measure the other configs")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--path", type=int, default=0, choices=(0, 1, 2),
+                   help="expert path: 0 the library's choice by T, 1 GEMV tiles, 2 MFMA tiles")
     p.add_argument("--graph", action="store_true",
                    help="replay a HIP graph of each step's kernels instead of launching them "
                         "directly (measured slower than direct launches on ROCm 7.2)")
@@ -110,19 +112,21 @@ def dominant_kernel(stage, T, path):
     """Kernel name of a stage on the path the library picks for T tokens."""
     if T == 1 and path == 0:
         return {"gateup": "k_gateup_decode", "down": "k_down_decode"}[stage]
-    mfma = path == 2 or (path == 0 and T >= 64)
+    mfma = path == 2 or (path == 0 and T >= 2)
     if mfma:
         return {"gateup": "k_moe_mfma<true>", "down": "k_moe_mfma<false>"}[stage]
     return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
 
 
-def measure(torch, H, C, cfg, steps, warmup, use_graph=False):
+def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0):
     layers = []
     for li in range(cfg.n_layers):
         L = H.MoELayer(cfg.T)
         L.synth_experts(cfg.weight_seed, li)
         nw, rt, b = C.config_tensors(cfg, li)
         L.set_router(nw, rt, b)
+        if path:
+            L.set_path(path)
         layers.append(L)
     x = torch.from_numpy(C.inputs(cfg.input_seed, cfg.T).copy()).cuda()
     stream = torch.cuda.current_stream().cuda_stream
@@ -249,7 +253,7 @@ def main():
     torch.cuda.init()
     cfg = C.CONFIGS[a.config]
     steps = a.steps or default_steps(cfg.T, cfg.n_layers)
-    r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph)
+    r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph, path=a.path)
     out = {
         "metric": "MoE-layer tokens/s (decode B=1) and achieved HBM GB/s vs peak",
         "value": round(r["tokens_per_s"], 2),
@@ -262,7 +266,8 @@ def main():
         "config": {"workload": f"config{cfg.index}:{cfg.name}", "tokens": cfg.T,
                    "layers": cfg.n_layers, "top_k": cfg.K, "experts": "192+1 shared",
                    "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu",
-                   "launch": "hip-graph" if a.graph else "direct"},
+                   "launch": "hip-graph" if a.graph else "direct",
+                   "expert_path": ["auto", "gemv", "mfma"][a.path]},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),
                   "hbm_frac": round(r["layer_GBps"] / PEAK_HBM_GBS, 4),
                   "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},

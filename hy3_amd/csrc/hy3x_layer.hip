@@ -110,9 +110,11 @@ constexpr int kSmallRouterT = 8;
 constexpr int kMidRouterT = 128;
 // Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
 constexpr int kLargeRouterT = 512;
-// From this many tokens the experts run as MFMA grouped GEMMs, below it as
-// wavefront-reduction GEMVs.
-constexpr int kMfmaMinT = 64;
+// From this many tokens the experts run as MFMA grouped GEMMs. Measured on MI355X the
+// MFMA tiles beat the wavefront-reduction GEMV tiles at every T >= 2 (T=2: 51 vs 66 us,
+// T=32: 442 vs 550 us for gate/up + down), so the GEMV tiles only run when selected
+// explicitly (hy3x_layer_set_path 1); T = 1 keeps the fused decode kernels.
+constexpr int kMfmaMinT = 2;
 
 static int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
