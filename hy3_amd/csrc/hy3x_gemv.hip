@@ -168,17 +168,25 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = blockIdx.x / DEC_GU_BLOCKS, rc = blockIdx.x % DEC_GU_BLOCKS;
-  // the token's staged s, once per block (the four waves read it from LDS)
+  // the token's staged s, once per block (the four waves read it from LDS),
+  // loaded together with the routing inputs
+  const int tid = threadIdx.x;
+  const uint4 sa = reinterpret_cast<const uint4 *>(s16)[tid];
+  const uint4 sb = reinterpret_cast<const uint4 *>(s16)[tid + 256];
   __shared__ __attribute__((aligned(16))) __half s_l[D];
-  reinterpret_cast<uint4 *>(s_l)[threadIdx.x] = reinterpret_cast<const uint4 *>(s16)[threadIdx.x];
-  reinterpret_cast<uint4 *>(s_l)[threadIdx.x + 256] =
-      reinterpret_cast<const uint4 *>(s16)[threadIdx.x + 256];
   __shared__ int32_t sids[KMAX], scratch_l[4 * E + 2 * KMAX + 2];
-  __shared__ __attribute__((aligned(16))) float swp[KMAX], sw[KMAX], sc_l[E], sg_l[E];
-  topk_block(sig, score, K, scale, sids, swp, sw, sc_l, sg_l, scratch_l);  // has barriers
-  trace_point(trace, 1);
+  __shared__ float swp[KMAX], sw[KMAX], sg_l[E];
+  reinterpret_cast<uint4 *>(s_l)[tid] = sa;
+  reinterpret_cast<uint4 *>(s_l)[tid + 256] = sb;
+  // s_l is visible after topk_block's first barrier; waves 1-3 unpack their
+  // s groups while wave 0 finishes the routing
+  topk_block<false>(sig, score, K, scale, sids, swp, sw, sg_l, scratch_l, trace);
   uint32_t X[32];
   load_group_x(s_l, lane, X);
+  float slo, shi;
+  group_sums(X, slo, shi);
+  __syncthreads();
+  trace_point(trace, 1);
   const int e = sids[slot];
   if (blockIdx.x == 0) {
     if (threadIdx.x < K) {
@@ -191,8 +199,6 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
       stats[1] += (unsigned long long)(K + 1);
     }
   }
-  float slo, shi;
-  group_sums(X, slo, shi);
   gateup_rows<DEC_RPW, DEC_GU_PF>(wq, e, slot, rc * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
   trace_point(trace, 3);
 }

@@ -19,7 +19,7 @@ extern template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const f
 extern template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int,
                                                           float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
-                       int32_t *ids, float *wpre, float *wout);
+                       int T, int32_t *ids, float *wpre, float *wout);
 __global__ void k_dispatch_clear(int T, uint32_t *bits, int wt, int32_t *dcount);
 __global__ void k_dispatch_mark(const int32_t *ids, int T, int K, uint32_t *bits, int wt,
                                 int32_t *dcount);

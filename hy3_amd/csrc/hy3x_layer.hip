@@ -260,8 +260,8 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
           k_router_gemm<8, 4, 4, 8><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
       }
-      k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, L->ids, L->wpre,
-                                L->w);
+      k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, T,
+                                          L->ids, L->wpre, L->w);
       break;
     case HY3X_STAGE_DISPATCH:
       if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);

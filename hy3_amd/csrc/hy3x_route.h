@@ -88,26 +88,21 @@ __device__ __forceinline__ void wave_best(float &v, int &key) {
   key = bk;
 }
 
-// Top-K of one token by one wave from its 192 sigmoid values and biased
-// scores (hy3.c:1282-1291): selection with swaps (each step takes the largest
-// score, ties to the lowest current position, and the element at position k
-// moves to the winner's position), then w_k = sigma_k * (1/(sum + 1e-20)).
-// Scores sit 3 per lane (expert e at lane e%64, slot e/64). sig_l and
-// sel_l are LDS scratch (192 and 8 entries). Lane 0 writes ids/wpre/wout.
-__device__ __forceinline__ void topk_wave(const float *sig, const float *score, int K, float scale,
-                                          int32_t *ids, float *wpre, float *wout, float *sig_l,
-                                          int32_t *sel_l) {
+// Top-K of one token by one wave (hy3.c:1282-1291). Expert e sits at lane
+// e % 64, slot e / 64 of sc (biased score) and sg (sigmoid). Selection with
+// swaps: step k takes the largest score among positions >= k, ties to the
+// lowest current position, and the element at position k moves to the
+// winner's position. Then sum = sigma_sel0 + sigma_sel1 + ... in selection
+// order, inv = 1 / (sum + 1e-20), wpre_k = sigma_k * inv, w_k = wpre_k * scale.
+// Everything stays in registers; lane k < K writes ids[k], wpre[k], wout[k].
+__device__ __forceinline__ void topk_wave_regs(const float (&sc)[3], const float (&sg)[3], int K,
+                                               float scale, int32_t *ids, float *wpre,
+                                               float *wout) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  float sc[3];
-  int pos[3];
-#pragma unroll
-  for (int m = 0; m < 3; m++) {
-    const int e = lane + 64 * m;
-    sc[m] = score[e];
-    if (sig_l != sig) sig_l[e] = sig[e];
-    pos[m] = e;
-  }
+  int pos[3] = {lane, lane + 64, lane + 128};
+  float sum = 0.0f, my_sig = 0.0f;
+  int my_e = 0;
   for (int k = 0; k < K; k++) {
     float bv = -__builtin_huge_valf();
     int bk = 0x7fffffff;
@@ -126,163 +121,93 @@ __device__ __forceinline__ void topk_wave(const float *sig, const float *score, 
       if (pos[m] == k) pos[m] = bp;               // the element at position k moves
       if (lane + 64 * m == be) pos[m] = k;        // the winner takes position k
     }
-    if (lane == 0) sel_l[k] = be;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  if (lane == 0) {
-    float sum = 0.0f;
-    for (int k = 0; k < K; k++) sum += sig_l[sel_l[k]];
-    const float inv = 1.0f / (sum + 1e-20f);
-    for (int k = 0; k < K; k++) {
-      const int e = sel_l[k];
-      const float v = sig_l[e] * inv;
-      ids[k] = e;
-      wpre[k] = v;
-      wout[k] = v * scale;
+    const int bm = be >> 6;
+    const float sv = bm == 0 ? sg[0] : (bm == 1 ? sg[1] : sg[2]);
+    const float s_be =
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), be & 63));
+    sum = sum + s_be;
+    if (lane == k) {
+      my_e = be;
+      my_sig = s_be;
     }
   }
+  const float inv = 1.0f / (sum + 1e-20f);
+  if (lane < K) {
+    const float v = my_sig * inv;
+    ids[lane] = my_e;
+    wpre[lane] = v;
+    wout[lane] = v * scale;
+  }
 }
 
-// Order-preserving unsigned key of a float score (-0.0 folded into +0.0 so
-// that equal scores have equal keys).
-__device__ __forceinline__ uint32_t score_key(float v) {
-  const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ int wave_count_ge(const uint32_t (&key)[3], uint32_t t) {
-  return __builtin_popcountll(__ballot(key[0] >= t)) + __builtin_popcountll(__ballot(key[1] >= t)) +
-         __builtin_popcountll(__ballot(key[2] >= t));
-}
-
-// Top-K by one wave without a sequential selection: bisection on the score
-// keys finds the largest threshold with K scores at or above it; the K
-// selected scores, if distinct from each other and from every unselected
-// score, are picked by selection-with-swaps in descending order, so each one's
-// rank among them is its slot. Ties at or above the threshold, or a NaN, use
-// the sequential selection (topk_wave), which defines the result then.
-// Writes ids/wpre/wout (lane 0) like topk_wave; sig_l, sel_l: LDS scratch.
-__device__ __forceinline__ void topk_ballot(const float *sig, const float *score, int K,
-                                            float scale, int32_t *ids, float *wpre, float *wout,
-                                            float *sig_l, int32_t *sel_l,
-                                            unsigned long long *trace = nullptr) {
-#pragma clang fp contract(off)
+// The same from 192-entry arrays sig / score (global or LDS).
+__device__ __forceinline__ void topk_wave(const float *sig, const float *score, int K, float scale,
+                                          int32_t *ids, float *wpre, float *wout) {
   const int lane = threadIdx.x & 63;
-  uint32_t key[3];
-  float sg[3];
-  bool nan = false;
+  float sc[3], sg[3];
 #pragma unroll
   for (int m = 0; m < 3; m++) {
-    const float v = score[lane + 64 * m];
+    sc[m] = score[lane + 64 * m];
     sg[m] = sig[lane + 64 * m];
-    nan |= v != v;
-    key[m] = score_key(v);
   }
-  if (trace) {
-    __builtin_amdgcn_s_waitcnt(0);
-    trace_point(trace, 4);
-  }
-  // largest t with count(key >= t) >= K (count(key >= 0) = 192 >= K holds
-  // initially; the interval halves every step, so 32 steps finish it)
-  uint64_t lo = 0ull, hi = 0xFFFFFFFFull;
-  for (int it = 0; it < 33 && lo < hi; it++) {
-    const uint64_t mid = (lo + hi + 1ull) >> 1;
-    if (wave_count_ge(key, (uint32_t)mid) >= K) lo = mid; else hi = mid - 1ull;
-  }
-  const uint32_t thr = (uint32_t)lo;
-  if (trace) trace_point(trace, 5);
-  const bool exact = wave_count_ge(key, thr) == K && __ballot(nan) == 0ull;
-  bool distinct = exact;
-  if (exact) {
-    // rank of each selected score among the selected ones
-#pragma unroll
-    for (int m = 0; m < 3; m++) {
-      const bool mine = key[m] >= thr;
-      int above = 0, equal = 0;
-      const unsigned long long selm[3] = {__ballot(key[0] >= thr), __ballot(key[1] >= thr),
-                                          __ballot(key[2] >= thr)};
-      // compare against every selected key (at most K of them)
-      for (int mm = 0; mm < 3; mm++) {
-        unsigned long long msk = selm[mm];
-        while (msk) {
-          const int src = __builtin_ctzll(msk);
-          msk &= msk - 1ull;
-          const uint32_t kv = (uint32_t)__builtin_amdgcn_readlane((int)key[mm], src);
-          above += kv > key[m];
-          equal += (kv == key[m]) && !(src == lane && mm == m);
-        }
-      }
-      if (mine) {
-        if (equal) distinct = false;
-        sel_l[above] = lane + 64 * m;
-        sig_l[lane + 64 * m] = sg[m];
-      }
-    }
-    distinct = __ballot(!distinct) == 0ull;
-  }
-  if (!distinct) {
-    topk_wave(sig, score, K, scale, ids, wpre, wout, sig_l, sel_l);
-    return;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  if (lane == 0) {
-    float sum = 0.0f;
-    for (int k = 0; k < K; k++) sum += sig_l[sel_l[k]];
-    const float inv = 1.0f / (sum + 1e-20f);
-    for (int k = 0; k < K; k++) {
-      const int e = sel_l[k];
-      const float v = sig_l[e] * inv;
-      ids[k] = e;
-      wpre[k] = v;
-      wout[k] = v * scale;
-    }
-  }
+  topk_wave_regs(sc, sg, K, scale, ids, wpre, wout);
 }
 
-// Top-K by a 256-thread block: thread t counts, for elements i = t, t+256..
-// (i < 192 x 4 comparator quarters), the scores of quarter t/192.. greater
-// than score i; the four partial ranks are summed in LDS. With distinct top
-// scores, selection-with-swaps picks in descending score order, so the element
-// of rank k is the k-th pick. Any tie among the first K ranks (two elements
-// with one rank, or a rank left empty) or a NaN sends wave 0 to the
-// sequential selection, which defines the result then. sc_l/sg_l: LDS (192
-// each); scratch_l: LDS int[4*192 + 2*KMAX + 2]; ids/wpre/w: LDS or global.
-// Every thread must call it; it ends with a barrier.
+// Top-K by a 256-thread block, with the same result as topk_wave_regs.
+// Rank of element e = number of scores strictly greater than score[e]: wave w
+// holds quarter w (scores 48w .. 48w+47) as wave-uniform values and counts,
+// for each of its lanes' three elements (lane + 64 m), how many of them are
+// greater; the four partial counts are summed in LDS. With distinct top
+// scores, selection with swaps picks in descending score order, so the
+// element of rank k is the k-th pick. Any tie among the first K ranks (two
+// elements with one rank, or a rank left empty) or a NaN sends wave 0 to the
+// sequential selection, which defines the result then.
+// sig / score: 192 entries each (global or LDS; visible to the whole block).
+// sg_l: LDS float[192]; scratch_l: LDS int[4*192 + 2*KMAX + 2]. ids_l, wpre_l,
+// w_l: outputs (LDS or global), valid after the call, which ends with a
+// barrier unless kFinalBarrier is false (then the caller's next barrier makes
+// them visible). Every thread must call it; after it, no global memory is read.
+template <bool kFinalBarrier = true>
 __device__ __forceinline__ void topk_block(const float *sig, const float *score, int K, float scale,
-                                           int32_t *ids_l, float *wpre_l, float *w_l,
-                                           float *sc_l, float *sg_l, int32_t *scratch_l) {
+                                           int32_t *ids_l, float *wpre_l, float *w_l, float *sg_l,
+                                           int32_t *scratch_l,
+                                           unsigned long long *trace = nullptr) {
 #pragma clang fp contract(off)
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int32_t *part_l = scratch_l, *cnt_l = scratch_l + 4 * E, *flag_l = cnt_l + KMAX,
           *sel_l = flag_l + 1;
-  if (tid < E) {
-    sc_l[tid] = score[tid];
-    sg_l[tid] = sig[tid];
-  }
+  // every load first: the lane's three elements, the wave's quarter, sigma
+  float v[3];
+#pragma unroll
+  for (int m = 0; m < 3; m++) v[m] = score[lane + 64 * m];
+  float4 q4[12];
+  const float4 *qsrc = reinterpret_cast<const float4 *>(score + 48 * wave);
+#pragma unroll
+  for (int u = 0; u < 12; u++) q4[u] = qsrc[u];
+  const float sgv = tid < E ? sig[tid] : 0.0f;
   if (tid < KMAX) cnt_l[tid] = 0;
   if (tid == 0) *flag_l = 0;
-  __syncthreads();
-  // (element, quarter) pairs q = tid + 256 j, j < 3: element q % 192, quarter q / 192
+  int cnt[3] = {0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < 3; j++) {
-    const int q = tid + 256 * j, i = q % E, c = q / E;
-    const float s = sc_l[i];
-    const float4 *v4 = reinterpret_cast<const float4 *>(sc_l + 48 * c);
-    int rank = 0;
+  for (int u = 0; u < 12; u++) {
+    const float qx = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].x)));
+    const float qy = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].y)));
+    const float qz = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].z)));
+    const float qw = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].w)));
 #pragma unroll
-    for (int u = 0; u < 12; u++) {
-      const float4 v = v4[u];
-      rank += (v.x > s) + (v.y > s) + (v.z > s) + (v.w > s);
-    }
-    part_l[q] = rank;
+    for (int m = 0; m < 3; m++)
+      cnt[m] += (int)(qx > v[m]) + (int)(qy > v[m]) + (int)(qz > v[m]) + (int)(qw > v[m]);
   }
+#pragma unroll
+  for (int m = 0; m < 3; m++) part_l[wave * E + lane + 64 * m] = cnt[m];
+  if (tid < E) sg_l[tid] = sgv;
   __syncthreads();
+  if (trace) trace_point(trace, 4);
   if (tid < E) {
     const int rank = (part_l[tid] + part_l[tid + E]) + (part_l[tid + 2 * E] + part_l[tid + 3 * E]);
-    const float s = sc_l[tid];
-    if (s != s) atomicOr(flag_l, 1);
+    const float sv = wave == 0 ? v[0] : (wave == 1 ? v[1] : v[2]);  // score[tid]
+    if (sv != sv) atomicOr(flag_l, 1);
     if (rank < K) {
       atomicAdd(&cnt_l[rank], 1);
       sel_l[rank] = tid;
@@ -291,21 +216,24 @@ __device__ __forceinline__ void topk_block(const float *sig, const float *score,
   __syncthreads();
   if (tid < K && cnt_l[tid] != 1) atomicOr(flag_l, 1);
   __syncthreads();
+  if (trace) trace_point(trace, 5);
   if (*flag_l) {
-    if (tid < 64) topk_wave(sg_l, sc_l, K, scale, ids_l, wpre_l, w_l, sg_l, sel_l);
-  } else if (tid == 0) {
+    if (wave == 0) topk_wave(sg_l, score, K, scale, ids_l, wpre_l, w_l);
+  } else if (wave == 0) {
+    const int e = lane < K ? sel_l[lane] : 0;
+    const float se = sg_l[e];
     float sum = 0.0f;
-    for (int k = 0; k < K; k++) sum += sg_l[sel_l[k]];
+    for (int k = 0; k < K; k++)
+      sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, se), k));
     const float inv = 1.0f / (sum + 1e-20f);
-    for (int k = 0; k < K; k++) {
-      const int e = sel_l[k];
-      const float v = sg_l[e] * inv;
-      ids_l[k] = e;
-      wpre_l[k] = v;
-      w_l[k] = v * scale;
+    if (lane < K) {
+      const float wv = se * inv;
+      ids_l[lane] = e;
+      wpre_l[lane] = wv;
+      w_l[lane] = wv * scale;
     }
   }
-  __syncthreads();
+  if (kFinalBarrier) __syncthreads();
 }
 
 // Sum of squares of a 4096-vector by a 256-thread block, thread t holding

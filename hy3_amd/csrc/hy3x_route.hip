@@ -303,23 +303,24 @@ template __global__ void k_router_gemm<4, 4, 4, 8>(const float *, const float *,
 template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int, float *);
 template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const float *, int, float *);
 
-// Routing of one token per block (large-T path): sigmoid and scores of the
+// Routing of one token per block (T > 1 paths): sigmoid and scores of the
 // 192 logits, then the top-K.
 __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
                                               const float *__restrict__ bias, int has_bias, int K,
-                                              float scale, int32_t *__restrict__ ids,
+                                              float scale, int T, int32_t *__restrict__ ids,
                                               float *__restrict__ wpre, float *__restrict__ wout) {
   const int t = blockIdx.x;
-  __shared__ __attribute__((aligned(16))) float sg[E], sc[E], sc_l[E], sg_l[E];
+  __shared__ __attribute__((aligned(16))) float sg[E], sc[E], sg_l[E];
   __shared__ int32_t scratch_l[4 * E + 2 * KMAX + 2];
-  for (int e = threadIdx.x; e < E; e += 256) {
+  if (threadIdx.x < E) {
+    const int e = threadIdx.x;
     const float v = sigmoid_c(logits[(size_t)t * E + e]);
     sg[e] = v;
     sc[e] = has_bias ? v + bias[e] : v;
   }
   __syncthreads();
   topk_block(sg, sc, K, scale, ids + (size_t)t * K, wpre + (size_t)t * K, wout + (size_t)t * K,
-             sc_l, sg_l, scratch_l);
+             sg_l, scratch_l);
 }
 
 // Device dispatch: per-expert slot lists and the work-tile list.
