@@ -39,6 +39,7 @@
 // staged in that order (perm8).
 #include "hy3x_kernels.h"
 #include "hy3x_q4k.h"
+#include "hy3x_dma.h"
 
 namespace hy3x {
 
@@ -46,7 +47,6 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));  // 16 bytes as a native vector
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int MT_TOK = 32;                 // tokens per tile (dispatch NT for this path)
 constexpr int MT_WAVES = MFMA_WAVES;       // waves per workgroup
@@ -78,31 +78,15 @@ __shared__ __attribute__((aligned(16))) u4_t bt_st[2][MT_TOK][32];
 __shared__ __attribute__((aligned(16))) u4_t bm_st[2][MT_TOK][4];
 __shared__ int32_t t_slot[MT_TOK], t_arow[MT_TOK];
 
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const lds_void_t *)p;
-}
-
-// 16-byte global -> LDS copy: lane i of the wave writes LDS bytes
-// [m0 + 16 i, m0 + 16 i + 16) (m0 = lds, wave-uniform). dma16_stream is the
-// weight copy; HY3X_WEIGHT_POLICY can add a cache-policy suffix to it (the
-// default caching measured best: a non-temporal " nt" was ~15% slower).
-__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
-}
+// dma16_stream is the weight copy (dma16 with an optional cache policy):
+// HY3X_WEIGHT_POLICY can add a policy suffix to it (the default caching
+// measured best: a non-temporal " nt" was ~15% slower).
 #ifndef HY3X_WEIGHT_POLICY
 #define HY3X_WEIGHT_POLICY ""
 #endif
 __device__ __forceinline__ void dma16_stream(const void *src, uint32_t lds) {
   asm volatile("global_load_lds_dwordx4 %0, off" HY3X_WEIGHT_POLICY ::"v"(src), "{m0}"(lds)
                : "memory");
-}
-
-// Wait until at most N of this wave's vector-memory operations are in flight
-// and all its LDS operations are done, then the workgroup barrier.
-template <int N>
-__device__ __forceinline__ void wait_copies_and_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt immediate");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, h2_t b, h2_t c) {
