@@ -9,7 +9,11 @@ hy3_amd/libhy3x.so. Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                             no packed-fp32 instructions are
                                             generated (they are unreliable on
-                                            the target machines).
+                                            the target machines);
+  -mllvm -amdgpu-mfma-vgpr-form             MFMA accumulators in VGPRs (no
+                                            copies between accumulation and
+                                            vector registers around the
+                                            per-block scale FMAs).
 HY3X_EXTRA_FLAGS (environment) appends flags, e.g. the tile-shape macros of
 hy3x_mfma.hip for tuning runs.
 """
@@ -29,6 +33,7 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
 ] + os.environ.get("HY3X_EXTRA_FLAGS", "").split()  # e.g. "-DHY3X_MFMA_WAVES=8" (tuning runs)
 

@@ -21,6 +21,12 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
+// The same with a wave-uniform base (scalar registers) and a per-lane 32-bit
+// byte offset: the address costs no vector instruction.
+__device__ __forceinline__ void dma16_s(const void *sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight.
 // Copies complete in issue order, so this makes the wave's first copies
 // (all but the last N) visible to the wave itself.

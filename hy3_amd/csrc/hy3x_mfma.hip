@@ -84,8 +84,9 @@ __shared__ int32_t t_slot[MT_TOK], t_arow[MT_TOK];
 #ifndef HY3X_WEIGHT_POLICY
 #define HY3X_WEIGHT_POLICY ""
 #endif
-__device__ __forceinline__ void dma16_stream(const void *src, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, off" HY3X_WEIGHT_POLICY ::"v"(src), "{m0}"(lds)
+__device__ __forceinline__ void dma16_stream(const void *sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" HY3X_WEIGHT_POLICY ::"v"(voff), "s"(sbase),
+               "{m0}"(lds)
                : "memory");
 }
 
@@ -165,16 +166,20 @@ struct MfmaCfg {
   static_assert(TROWS * NMAT == RB, "row-blocks per tile");
 };
 
-// Per-thread copy sources of one work tile (column 0; column kb adds kb
-// blocks).
+// Copy sources of one work tile: wave-uniform bases (scalar registers) plus
+// per-lane byte offsets, so that a copy costs no vector instruction. Column
+// kb adds kb blocks to the bases.
 template <bool GATEUP, int NTT>
 struct TileState {
   using C = MfmaCfg<GATEUP>;
   static constexpr int RG = C::RG, NMAT = C::NMAT;
-  const uint8_t *asrc[A_DMA];   // weight chunks
+  const uint8_t *abase;         // the expert's weights (uniform)
+  uint32_t aoff[A_DMA];         // weight chunks, from abase
   bool a_last;                  // the half-used last weight copy is active in this lane
-  const __half *bsrc[B_DMA];    // activation chunks
-  const __half *ssrc;           // sums chunk (lanes below S_LANES)
+  const uint8_t *bbase;         // activations (uniform)
+  uint32_t boff[B_DMA];         // activation chunks, from bbase
+  const uint8_t *sbase;         // sums (uniform)
+  uint32_t soff;                // sums chunk (lanes below S_LANES), from sbase
   f4_t acc[RG][NMAT][NTT];
 };
 
@@ -183,25 +188,24 @@ struct TileState {
 // wave, weights last.
 template <bool GATEUP, int NTT>
 __device__ __forceinline__ void issue_b(const TileState<GATEUP, NTT> &st, int kb) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int buf = kb & 1;
+  const uint8_t *bb = st.bbase + (size_t)kb * QK * 2;
 #pragma unroll
   for (int j = 0; j < B_DMA; j++)
-    dma16(st.bsrc[j] + kb * QK,
-          __builtin_amdgcn_readfirstlane(lds_addr(&bt_st[buf][0][0] + 64 * (B_DMA * wave + j))));
+    dma16_s(bb, st.boff[j], lds_addr(&bt_st[buf][0][0] + 64 * (B_DMA * wave + j)));
   if (lane < S_LANES)
-    dma16(st.ssrc + kb * 32,
-          __builtin_amdgcn_readfirstlane(lds_addr(&bm_st[buf][0][0] + S_LANES * wave)));
+    dma16_s(st.sbase + (size_t)kb * 64, st.soff,
+            lds_addr(&bm_st[buf][0][0] + S_LANES * wave));
 }
 template <bool GATEUP, int NTT>
 __device__ __forceinline__ void issue_a(const TileState<GATEUP, NTT> &st, int ka) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const u4_t *dst = &a_ring[ka % A_STAGES][0] + A_CHUNKS_WAVE * wave;
+  const uint8_t *ab = st.abase + (size_t)ka * QB;
 #pragma unroll
   for (int j = 0; j < A_DMA; j++)
-    if (j < A_DMA - 1 || st.a_last)
-      dma16_stream(st.asrc[j] + (size_t)ka * QB,
-                   __builtin_amdgcn_readfirstlane(lds_addr(dst + 64 * j)));
+    if (j < A_DMA - 1 || st.a_last) dma16_stream(ab, st.aoff[j], lds_addr(dst + 64 * j));
 }
 
 // One block column kb. Its copies were issued one (activations) and A_AHEAD
@@ -327,14 +331,14 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
 
   // weights: wave w copies chunks [288 w, 288 w + 288) of the column's
   // (row-block c / 9, 16-byte piece c % 9), 64 per copy
-  const uint8_t *ebase = wq + (size_t)e * EXPERT_BYTES;
+  st.abase = wq + (size_t)__builtin_amdgcn_readfirstlane(e) * EXPERT_BYTES;
 #pragma unroll
   for (int j = 0; j < A_DMA; j++) {
     int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
     if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
     const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
     const int m = GATEUP ? rb / RB_HALF : 2, lrow = GATEUP ? rb % RB_HALF : rb;
-    st.asrc[j] = ebase + (size_t)m * MAT_BYTES + (size_t)(rt * C::TROWS + lrow) * NKB * QB + 16 * pc;
+    st.aoff[j] = (uint32_t)(m * MAT_BYTES + (rt * C::TROWS + lrow) * NKB * QB + 16 * pc);
   }
   st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
   // activations: copy j of wave w fills positions q = 64 (B_DMA w + j) + lane
@@ -344,16 +348,18 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
   // part (q % 4) ^ ((row >> 2) & 3). Rows past n copy token 0's row (their D
   // rows are never stored).
   const int arow0 = t_arow[0];
+  st.bbase = reinterpret_cast<const uint8_t *>(act);
+  st.sbase = reinterpret_cast<const uint8_t *>(act_sum);
 #pragma unroll
   for (int j = 0; j < B_DMA; j++) {
     const int q = 64 * (B_DMA * wave + j) + lane, r = q >> 5;
     const int ar = t_arow[r] >= 0 ? t_arow[r] : arow0;
-    st.bsrc[j] = act + (size_t)ar * KD + 8 * ((q & 31) ^ (r & 15));
+    st.boff[j] = (uint32_t)(2 * (ar * KD + 8 * ((q & 31) ^ (r & 15))));
   }
   {
     const int q = S_LANES * wave + (lane & (S_LANES - 1)), r = q >> 2;
     const int ar = t_arow[r] >= 0 ? t_arow[r] : arow0;
-    st.ssrc = act_sum + (size_t)ar * C::NSUB * 4 + 8 * ((q & 3) ^ ((r >> 2) & 3));
+    st.soff = (uint32_t)(2 * (ar * C::NSUB * 4 + 8 * ((q & 3) ^ ((r >> 2) & 3))));
   }
   const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
