@@ -307,15 +307,36 @@ __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
 }
 
 // y = x + (shared + sum_k w_k * routed_k), k in selection order (hy3.c:1302,
-// 1318-1319, 1324-1325).
+// 1318-1319, 1324-1325). Block (c, t): elements 1024 c .. 1024 c + 1023 of
+// token t, four per thread; every slot's row is loaded before the FMA chain.
 __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
                                                  const float *__restrict__ out,
                                                  const float *__restrict__ w, int T, int K) {
-  const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-  float eo = 0.0f;
-  for (int k = 0; k < K; k++) eo = __builtin_fmaf(w[t * K + k], out[(size_t)(t * K + k) * D + i], eo);
-  const float sh = out[(size_t)(T * K + t) * D + i];
-  x[(size_t)t * D + i] = x[(size_t)t * D + i] + (sh + eo);
+  const int t = blockIdx.y, i = blockIdx.x * 1024 + 4 * threadIdx.x;
+  float4 r[KMAX];
+  float wk[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; k++)
+    if (k < K) {
+      r[k] = *reinterpret_cast<const float4 *>(out + (size_t)(t * K + k) * D + i);
+      wk[k] = w[t * K + k];
+    }
+  const float4 sh = *reinterpret_cast<const float4 *>(out + (size_t)(T * K + t) * D + i);
+  float4 xv = *reinterpret_cast<const float4 *>(x + (size_t)t * D + i);
+  float4 eo = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k = 0; k < KMAX; k++)
+    if (k < K) {
+      eo.x = __builtin_fmaf(wk[k], r[k].x, eo.x);
+      eo.y = __builtin_fmaf(wk[k], r[k].y, eo.y);
+      eo.z = __builtin_fmaf(wk[k], r[k].z, eo.z);
+      eo.w = __builtin_fmaf(wk[k], r[k].w, eo.w);
+    }
+  xv.x = xv.x + (sh.x + eo.x);
+  xv.y = xv.y + (sh.y + eo.y);
+  xv.z = xv.z + (sh.z + eo.z);
+  xv.w = xv.w + (sh.w + eo.w);
+  *reinterpret_cast<float4 *>(x + (size_t)t * D + i) = xv;
 }
 
 template __global__ void k_gateup_gemv<1>(const uint8_t *, const __half *, const int32_t *,

@@ -7,8 +7,9 @@ namespace hy3x {
 __global__ void k_router_logits(const float *x, const float *norm_w, const float *router,
                                 const float *bias, int has_bias, float *logits, float *sig,
                                 float *score, __half *s16, float *s32,
-                                unsigned long long *trace);
-__global__ void k_rmsnorm(const float *x, const float *norm_w, __half *s16, float *s32);
+                                unsigned long long *trace, int T, uint32_t *bits, int wt);
+__global__ void k_rmsnorm(const float *x, const float *norm_w, __half *s16, float *s32,
+                          __half *s16m, __half *ssum, int T, uint32_t *bits, int wt);
 template <int MT, int ME, int TG, int EG>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
                                                      float *logits);
@@ -19,12 +20,9 @@ extern template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const f
 extern template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int,
                                                           float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
-                       int T, int32_t *ids, float *wpre, float *wout);
-__global__ void k_dispatch_clear(int T, uint32_t *bits, int wt, int32_t *dcount);
-__global__ void k_dispatch_mark(const int32_t *ids, int T, int K, uint32_t *bits, int wt,
-                                int32_t *dcount);
+                       int T, int32_t *ids, float *wpre, float *wout, uint32_t *bits, int wt);
 __global__ void k_dispatch_list(const int32_t *ids, int T, int K, int NT, const uint32_t *bits,
-                                int wt, const int32_t *dcount, int32_t *list, int4 *tiles,
+                                int wt, int32_t *list, int4 *tiles,
                                 int32_t *n_tiles, int max_tiles, int32_t *counts_out,
                                 unsigned long long *stats);
 template <int NT>

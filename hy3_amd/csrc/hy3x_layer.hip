@@ -38,8 +38,7 @@ struct hy3x_layer {
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
   uint32_t *bits = nullptr;    // dispatch: per-expert token bitmaps [E][wt]
-  int32_t *dcount = nullptr;   // dispatch: per-expert slot counts
-  int wt = 0;                  // bitmap words per expert (max_tokens / 32, rounded up)
+  int wt = 0;                  // bitmap words per expert (max_tokens / 32, rounded up to 4)
   unsigned long long *stats = nullptr;
   int max_tiles_alloc = 0;
   int last_T = 0, last_K = 0;
@@ -134,7 +133,7 @@ int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
   void *ptrs[] = {L->wq, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
                   L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m, L->ssum, L->hsum, L->h16,     L->ids,     L->list,
-                  L->n_tiles, L->counts, L->tiles, L->bits, L->dcount, L->stats};
+                  L->n_tiles, L->counts, L->tiles, L->bits, L->stats};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   for (hipEvent_t ev : L->ev_pool) (void)hipEventDestroy(ev);
@@ -152,7 +151,7 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
   L->max_tokens = max_tokens;
   const size_t T = (size_t)max_tokens, slots = T * (KMAX + 1);
   L->max_tiles_alloc = max_tiles_for(max_tokens, KMAX, 1);
-  L->wt = (max_tokens + 31) / 32;
+  L->wt = ((max_tokens + 31) / 32 + 3) & ~3;  // 16-byte rows
   int rc = HY3X_OK;
   if ((rc = dalloc(&L->wq, (size_t)(E + 1) * EXPERT_BYTES)) ||
       (rc = dalloc(&L->norm_w, D * sizeof(float))) ||
@@ -177,13 +176,11 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
       (rc = dalloc(&L->n_tiles, sizeof(int32_t))) ||
       (rc = dalloc(&L->counts, (E + 1) * sizeof(int32_t))) ||
       (rc = dalloc(&L->bits, (size_t)E * L->wt * sizeof(uint32_t))) ||
-      (rc = dalloc(&L->dcount, E * sizeof(int32_t))) ||
       (rc = dalloc(&L->stats, 2 * sizeof(unsigned long long)))) {
     hy3x_layer_destroy(L);
     return rc;
   }
   if (hipMemset(L->bits, 0, (size_t)E * L->wt * sizeof(uint32_t)) != hipSuccess ||
-      hipMemset(L->dcount, 0, E * sizeof(int32_t)) != hipSuccess ||
       hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
       hipMemset(L->stats, 0, 2 * sizeof(unsigned long long)) != hipSuccess) {
     hy3x_layer_destroy(L);
@@ -244,12 +241,17 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
             L->s16, L->s32, L->wq, L->h16, L->trace[0]);
         break;
       }
+      // the routing kernels also clear (first kernel) and fill (top-K) the
+      // dispatch bitmaps; for T > 8 the RMSNorm kernel stages the MFMA operand
       if (T <= kSmallRouterT) {
         k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias,
                                                     L->has_bias, L->logits, L->sig, L->score,
-                                                    L->s16, L->s32, L->trace[0]);
+                                                    L->s16, L->s32, L->trace[0], T, L->bits,
+                                                    L->wt);
       } else {
-        k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, L->s16, L->s32);
+        const bool mf = c.mode == Mode::MFMA;
+        k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, mf ? nullptr : L->s16, L->s32,
+                                     mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt);
         if (T <= kMidRouterT)
           k_router_gemm<2, 2, 4, 8><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
@@ -260,17 +262,14 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
           k_router_gemm<8, 4, 4, 8><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
       }
-      k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, T,
-                                          L->ids, L->wpre, L->w);
+      k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, T, L->ids,
+                                L->wpre, L->w, L->bits, L->wt);
       break;
     case HY3X_STAGE_DISPATCH:
-      if (c.mode == Mode::MFMA) k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);
+      if (c.mode == Mode::MFMA && T <= kSmallRouterT)
+        k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);
       if (c.mode != Mode::DECODE) {
-        k_dispatch_clear<<<(E * ((T + 31) / 32) + 255) / 256, 256, 0, st>>>(T, L->bits, L->wt,
-                                                                           L->dcount);
-        k_dispatch_mark<<<(T * K + 255) / 256, 256, 0, st>>>(L->ids, T, K, L->bits, L->wt,
-                                                             L->dcount);
-        k_dispatch_list<<<E + 1, 256, 0, st>>>(L->ids, T, K, c.nt, L->bits, L->wt, L->dcount,
+        k_dispatch_list<<<E + 1, 256, 0, st>>>(L->ids, T, K, c.nt, L->bits, L->wt,
                                                L->list, L->tiles, L->n_tiles, mt, L->counts,
                                                L->stats);
       }
@@ -303,7 +302,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                       L->n_tiles, L->out);
       break;
     case HY3X_STAGE_COMBINE:
-      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 256, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 1024, T), 256, 0, st>>>(x, L->out, L->w, T, K);
       break;
   }
 }

@@ -118,4 +118,30 @@ __device__ __forceinline__ void load_group_x(const __half *staged, int g, uint32
   }
 }
 
+// Sub-block sums of one fp16 row of n32 * 32 values, as (Sh, Sl, Sh, Sl) with
+// Sh = fp16(sum), Sl = fp16(sum - Sh). One lane per sub-block.
+__device__ __forceinline__ void row_subsums(const __half *__restrict__ row, int n32,
+                                            __half *__restrict__ dst) {
+  for (int j = threadIdx.x; j < n32; j += blockDim.x) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(row + 32 * j);
+    float sum = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const uint4 q = src[v];
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const h2_t p = as_h2(w[u]);
+        sum += (float)p[0];
+        sum += (float)p[1];
+      }
+    }
+    const _Float16 hi = (_Float16)sum;
+    const _Float16 lo = (_Float16)(sum - (float)hi);
+    const h2_t r = {hi, lo};
+    *reinterpret_cast<h2_t *>(dst + 4 * j) = r;
+    *reinterpret_cast<h2_t *>(dst + 4 * j + 2) = r;
+  }
+}
+
 }  // namespace hy3x

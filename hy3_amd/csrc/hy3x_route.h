@@ -267,4 +267,26 @@ __device__ __forceinline__ void stage_store(__half *dst, int j, float v) {
   dst[stage_index(j)] = __float2half(v);
 }
 
+// Device dispatch, step 0 (in the first kernel of the routing): clear the
+// E x ceil(T/32) token-bitmap words of step 1. Part `part` of `nparts` (one
+// per block of that kernel) clears its share; a fill by kernels, not a
+// memset, so that the forward stays graph-capturable.
+__device__ __forceinline__ void dispatch_clear_part(int T, uint32_t *bits, int wt, int part,
+                                                    int nparts) {
+  const int nw = (T + 31) >> 5;
+  for (int f = part * 256 + (int)threadIdx.x; f < E * nw; f += nparts * 256)
+    bits[(f / nw) * wt + f % nw] = 0u;
+}
+
+// Step 1 (in the top-K kernel, once token t's ids are out): bit t of each of
+// its experts' token bitmaps (bits[e * wt + t / 32]). The result is
+// independent of the order of the atomics; step 2 counts by popcount.
+__device__ __forceinline__ void dispatch_mark(const int32_t *ids_t, int t, int K, uint32_t *bits,
+                                              int wt) {
+  if ((int)threadIdx.x < K) {
+    const int e = ids_t[threadIdx.x];
+    if (e >= 0 && e < E) atomicOr(&bits[(size_t)e * wt + (t >> 5)], 1u << (t & 31));
+  }
+}
+
 }  // namespace hy3x

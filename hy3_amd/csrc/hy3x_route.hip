@@ -129,7 +129,9 @@ __global__ __launch_bounds__(256) void k_router_logits(
     const float *__restrict__ x, const float *__restrict__ norm_w,
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
-    __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace) {
+    __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace, int T,
+    uint32_t *__restrict__ bits, int wt) {
+  if (bits) dispatch_clear_part(T, bits, wt, blockIdx.y * E + blockIdx.x, E * T);
   router_block(blockIdx.x, blockIdx.y, x, norm_w, router, bias, has_bias, logits, sig, score, s16,
                s32, trace);
 }
@@ -190,8 +192,12 @@ __global__ __launch_bounds__(256) void k_route_decode(
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
                                                  const float *__restrict__ norm_w,
                                                  __half *__restrict__ s16,
-                                                 float *__restrict__ s32) {
+                                                 float *__restrict__ s32,
+                                                 __half *__restrict__ s16m,
+                                                 __half *__restrict__ ssum, int T,
+                                                 uint32_t *__restrict__ bits, int wt) {
   const int t = blockIdx.x, tid = threadIdx.x;
+  if (bits) dispatch_clear_part(T, bits, wt, t, T);
   const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)t * D);
   const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
   float4 a[4];
@@ -206,10 +212,24 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
     const float4 sv = make_float4((a[u].x * w.x) * r, (a[u].y * w.y) * r, (a[u].z * w.z) * r,
                                   (a[u].w * w.w) * r);
     reinterpret_cast<float4 *>(s32 + (size_t)t * D)[tid + 256 * u] = sv;
-    stage_store(s16 + (size_t)t * D, j + 0, sv.x);
-    stage_store(s16 + (size_t)t * D, j + 1, sv.y);
-    stage_store(s16 + (size_t)t * D, j + 2, sv.z);
-    stage_store(s16 + (size_t)t * D, j + 3, sv.w);
+    if (s16) {
+      stage_store(s16 + (size_t)t * D, j + 0, sv.x);
+      stage_store(s16 + (size_t)t * D, j + 1, sv.y);
+      stage_store(s16 + (size_t)t * D, j + 2, sv.z);
+      stage_store(s16 + (size_t)t * D, j + 3, sv.w);
+    }
+    if (s16m) {  // fp16 in the MFMA run order (perm8: j + (0, 2, 1, 3)), one 8-byte store
+      const __half2 a01 = __halves2half2(__float2half(sv.x), __float2half(sv.z));
+      const __half2 a23 = __halves2half2(__float2half(sv.y), __float2half(sv.w));
+      uint2 v;
+      v.x = __builtin_bit_cast(uint32_t, a01);
+      v.y = __builtin_bit_cast(uint32_t, a23);
+      *reinterpret_cast<uint2 *>(s16m + (size_t)t * D + j) = v;
+    }
+  }
+  if (s16m) {  // and its sub-block sums
+    __syncthreads();
+    row_subsums(s16m + (size_t)t * D, D / 32, ssum + (size_t)t * (D / 32) * 4);
   }
 }
 
@@ -308,7 +328,8 @@ template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const float *,
 __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
                                               const float *__restrict__ bias, int has_bias, int K,
                                               float scale, int T, int32_t *__restrict__ ids,
-                                              float *__restrict__ wpre, float *__restrict__ wout) {
+                                              float *__restrict__ wpre, float *__restrict__ wout,
+                                              uint32_t *__restrict__ bits, int wt) {
   const int t = blockIdx.x;
   __shared__ __attribute__((aligned(16))) float sg[E], sc[E], sg_l[E];
   __shared__ int32_t scratch_l[4 * E + 2 * KMAX + 2];
@@ -319,8 +340,11 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
     sc[e] = has_bias ? v + bias[e] : v;
   }
   __syncthreads();
-  topk_block(sg, sc, K, scale, ids + (size_t)t * K, wpre + (size_t)t * K, wout + (size_t)t * K,
-             sg_l, scratch_l);
+  __shared__ int32_t ids_l[KMAX];
+  topk_block(sg, sc, K, scale, ids_l, wpre + (size_t)t * K, wout + (size_t)t * K, sg_l,
+             scratch_l);
+  if (threadIdx.x < K) ids[(size_t)t * K + threadIdx.x] = ids_l[threadIdx.x];
+  if (bits) dispatch_mark(ids_l, t, K, bits, wt);
 }
 
 // Device dispatch: per-expert slot lists and the work-tile list.
@@ -345,48 +369,37 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int *tmp) {
   return base + incl - v;
 }
 
-// Step 0: clear the E x ceil(T/32) bitmap words and the counters of step 1
-// (a fill kernel, so the whole forward can be captured in a graph).
-__global__ __launch_bounds__(256) void k_dispatch_clear(int T, uint32_t *__restrict__ bits, int wt,
-                                                        int32_t *__restrict__ dcount) {
-  const int nw = (T + 31) >> 5;
-  const int f = blockIdx.x * 256 + threadIdx.x;
-  if (f < E * nw) bits[(f / nw) * wt + f % nw] = 0u;
-  if (f < E) dcount[f] = 0;
-}
-
-// Step 1, one thread per routed slot: bit t of expert e's token bitmap
-// (bits[e * wt + t / 32]) and expert e's count. Both results are independent
-// of the order of the atomics.
-__global__ __launch_bounds__(256) void k_dispatch_mark(const int32_t *__restrict__ ids, int T,
-                                                       int K, uint32_t *__restrict__ bits, int wt,
-                                                       int32_t *__restrict__ dcount) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= T * K) return;
-  const int e = ids[i], t = i / K;
-  if (e < 0 || e >= E) return;
-  atomicOr(&bits[(size_t)e * wt + (t >> 5)], 1u << (t & 31));
-  atomicAdd(&dcount[e], 1);
-}
-
 // Step 2, one block per expert (E + 1 blocks, the last is the shared expert):
 // list offset and first tile from exclusive scans of all counts, the expert's
 // tiles, and its slots in token order from its bitmap (popcount prefix sums).
 // Block E also writes the tile count, the per-expert counts and the stats.
 __global__ __launch_bounds__(256) void k_dispatch_list(
     const int32_t *__restrict__ ids, int T, int K, int NT, const uint32_t *__restrict__ bits,
-    int wt, const int32_t *__restrict__ dcount, int32_t *__restrict__ list,
+    int wt, int32_t *__restrict__ list,
     int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles, int max_tiles,
     int32_t *__restrict__ counts_out, unsigned long long *__restrict__ stats) {
-  __shared__ int tmp[8], off_l, toff_l;
+  __shared__ int tmp[8], off_l, toff_l, ce_l;
   const int e = blockIdx.x, tid = threadIdx.x;
-  const int c = tid < E ? dcount[tid] : (tid == E ? T : 0);
+  const int nw = (T + 31) >> 5;
+  // expert tid's count: the popcount of its token bitmap (every block forms
+  // all counts itself; no counter atomics in the marking step)
+  int c = tid == E ? T : 0;
+  if (tid < E) {  // rows are 16-byte aligned (wt % 4 == 0); words past nw are not counted
+    const uint4 *row = reinterpret_cast<const uint4 *>(bits + (size_t)tid * wt);
+    for (int q = 0; 4 * q < nw; q++) {
+      const uint4 v = row[q];
+      const int w = 4 * q;
+      c += __popc(v.x) + (w + 1 < nw ? __popc(v.y) : 0) + (w + 2 < nw ? __popc(v.z) : 0) +
+           (w + 3 < nw ? __popc(v.w) : 0);
+    }
+  }
   const int off = block_exclusive_scan256(c, tmp);
   const int nt = (c + NT - 1) / NT;
   const int toff = block_exclusive_scan256(nt, tmp);
   if (tid == e) {
     off_l = off;
     toff_l = toff;
+    ce_l = c;
   }
   if (e == E) {
     const int active = block_exclusive_scan256(c > 0 ? 1 : 0, tmp);
@@ -400,15 +413,13 @@ __global__ __launch_bounds__(256) void k_dispatch_list(
     if (counts_out && tid <= E) counts_out[tid] = c;
   }
   __syncthreads();
-  const int eoff = off_l, etoff = toff_l;
-  const int ce = e < E ? dcount[e] : T;
+  const int eoff = off_l, etoff = toff_l, ce = ce_l;
   for (int j = tid; j * NT < ce; j += 256)
     if (etoff + j < max_tiles) tiles[etoff + j] = make_int4(e, eoff + j * NT, min(NT, ce - j * NT), 0);
   if (e == E) {
     for (int t = tid; t < T; t += 256) list[eoff + t] = T * K + t;
     return;
   }
-  const int nw = (T + 31) >> 5;
   int base = 0;
   for (int w0 = 0; w0 < nw; w0 += 256) {  // rounds of 256 bitmap words, in order
     const int w = w0 + tid;
