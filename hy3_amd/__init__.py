@@ -27,6 +27,7 @@ SHARED = 192
 K_MAX = 8
 Q4K_BLOCK = 144
 Q4K_MATRIX_BYTES = 3538944
+Q8_0_MATRIX_BYTES = 7077888  # hy3's Q8_0: 36 bytes per 32 weights
 ROUTE_SCALE = 2.826
 # Tensor kinds of the synthetic-input specification.
 T_X, T_NORM, T_ROUTER, T_BIAS, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7
@@ -50,6 +51,9 @@ _SIGS = {
     "hy3x_layer_set_router": (I32, [P, P, P, P]),
     "hy3x_layer_set_expert_q4k": (I32, [P, I32, P, P, P, I32]),
     "hy3x_layer_expert_ptr": (I32, [P, I32, I32, ctypes.POINTER(P)]),
+    "hy3x_layer_set_shared_q8_0": (I32, [P, P, P, P, I32]),
+    "hy3x_synth_shared_q8_0": (I32, [P, U64, U32]),
+    "hy3x_synth_quantize_q8_0": (I32, [P, P, I64, P]),
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
@@ -167,6 +171,17 @@ class MoELayer:
 
     def synth_experts(self, seed, layer_index=0):
         _check(lib().hy3x_synth_layer_experts(self._h, seed, layer_index))
+
+    def set_shared_q8_0(self, gate, up, down, on_device=False):
+        """The shared expert in hy3's Q8_0 (36-byte blocks; hy3x_layer_set_shared_q8_0)."""
+        if not on_device:
+            gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+            assert gate.size == up.size == down.size == Q8_0_MATRIX_BYTES
+        _check(lib().hy3x_layer_set_shared_q8_0(self._h, _ptr(gate), _ptr(up), _ptr(down),
+                                                1 if on_device else 0))
+
+    def synth_shared_q8_0(self, seed, layer_index=0):
+        _check(lib().hy3x_synth_shared_q8_0(self._h, seed, layer_index))
 
     path = 0  # 0 auto, 1 GEMV, 2 MFMA (hy3x_layer_set_path)
 

@@ -12,6 +12,7 @@
 #include "hy3x_decode.h"
 #include "hy3x_route.h"
 #include "hy3x_dma.h"
+#include "hy3x_q8.h"
 
 namespace hy3x {
 
@@ -212,7 +213,9 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
 // h slot straight into LDS with every copy issued at once (2.25 waves per
 // SIMD cannot keep enough bytes in flight from registers), then computes
 // each pass of 2 rows as soon as the copies holding them have landed. The
-// row sums go to LDS and 16 threads combine them.
+// row sums go to LDS and 16 threads combine them. wsh != nullptr: the shared
+// expert is the layer's Q8 one (hy3x_q8.h); its wave streams its rows (twice
+// the bytes, more than its LDS share holds) through registers instead.
 namespace {
 constexpr int DN_ROWB = (F / QK) * QB;                          // 864 B per down row
 constexpr int DN_WB = DEC_DOWN_RPB * DN_ROWB;                   // 13,824 B per wave
@@ -265,7 +268,7 @@ __device__ __forceinline__ void down_passes(const uint8_t *wl, const uint32_t (&
 __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
     const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
-    float *__restrict__ x, unsigned long long *trace) {
+    float *__restrict__ x, const uint8_t *__restrict__ wsh, unsigned long long *trace) {
   constexpr int RPB = DEC_DOWN_RPB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[KMAX + 1][DN_WAVE_B];
   __shared__ float out_l[KMAX + 1][RPB];
@@ -273,7 +276,14 @@ __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
   const int lane = threadIdx.x & 63;
   const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r0 = blockIdx.x * RPB;
-  if (k <= K) {
+  if (k == K && wsh) {
+    down_rows_q8<RPB / 2, 2>(wsh, h16 + (size_t)K * F, r0, [&](int ps, float2 t) {
+      if (lane == 0) {
+        out_l[K][2 * ps] = t.x;
+        out_l[K][2 * ps + 1] = t.y;
+      }
+    });
+  } else if (k <= K) {
     const int e = k < K ? __builtin_amdgcn_readfirstlane(ids[k]) : E;
     uint8_t *hl = lds[k], *wl = lds[k] + 1024 * DN_NH;
     const uint8_t *hsrc = reinterpret_cast<const uint8_t *>(h16 + (size_t)k * F) + 16 * lane;

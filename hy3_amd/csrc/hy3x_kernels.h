@@ -39,9 +39,13 @@ __global__ void k_gateup_decode(const uint8_t *wq, const __half *s16, const floa
 __global__ void k_route_decode(const float *x, const float *norm_w, const float *router,
                                const float *bias, int has_bias, int K, float *logits,
                                float *sig, float *score, __half *s16, float *s32,
-                               const uint8_t *wq, __half *h16, unsigned long long *trace);
+                               const uint8_t *wq, const uint8_t *wsh, __half *h16,
+                               unsigned long long *trace);
 __global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *ids,
-                              const float *w, int K, float *x, unsigned long long *trace);
+                              const float *w, int K, float *x, const uint8_t *wsh,
+                              unsigned long long *trace);
+__global__ void k_repack_q8x128(const uint8_t *src, uint8_t *dst, int64_t n_super);
+__global__ void k_synth_q8_0(uint8_t *dst, int64_t nblocks, uint64_t key, const float *src);
 __global__ void k_combine(float *x, const float *out, const float *w, int T, int K);
 
 extern template __global__ void k_gateup_gemv<1>(const uint8_t *, const __half *, const int32_t *,

@@ -18,6 +18,7 @@
 #include "../../include/hy3x_moe.h"
 #include "hy3x_kernels.h"
 #include "hy3x_decode.h"
+#include "hy3x_q8.h"
 
 using namespace hy3x;
 
@@ -29,6 +30,8 @@ struct hy3x_layer {
   int device = 0;
   int max_tokens = 0;
   uint8_t *wq = nullptr;
+  uint8_t *wsh = nullptr;      // the shared expert in Q8 (q8x128 layout), when set
+  int shared_q8 = 0;           // 1: the forward uses wsh for the shared expert
   float *norm_w = nullptr, *router = nullptr, *bias = nullptr;
   int has_bias = 0, router_set = 0;
   float *logits = nullptr, *sig = nullptr, *score = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
@@ -131,7 +134,7 @@ int hy3x_set_device(int device) {
 
 int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
-  void *ptrs[] = {L->wq, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
+  void *ptrs[] = {L->wq, L->wsh, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
                   L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m, L->ssum, L->hsum, L->h16,     L->ids,     L->list,
                   L->n_tiles, L->counts, L->tiles, L->bits, L->stats};
   for (void *p : ptrs)
@@ -218,7 +221,52 @@ int hy3x_layer_set_expert_q4k(hy3x_layer *L, int expert, const void *gate, const
   HIP_TRY(hipMemcpy(dst, gate, MAT_BYTES, kind));
   HIP_TRY(hipMemcpy(dst + MAT_BYTES, up, MAT_BYTES, kind));
   HIP_TRY(hipMemcpy(dst + 2 * MAT_BYTES, down, MAT_BYTES, kind));
+  if (expert == E) L->shared_q8 = 0;  // the shared expert is this Q4_K one again
   return HY3X_OK;
+}
+
+static int ensure_wsh(hy3x_layer *L) {
+  if (L->wsh) return HY3X_OK;
+  if (hipMalloc(&L->wsh, Q8_EXPERT_BYTES) != hipSuccess)
+    return fail(HY3X_E_NOMEM, "hipMalloc of %lld bytes (Q8 shared expert) failed",
+                (long long)Q8_EXPERT_BYTES);
+  return HY3X_OK;
+}
+
+// hy3 Q8_0 matrix (device, 36-byte blocks) -> matrix m of wsh (q8x128).
+static int repack_q8(hy3x_layer *L, const uint8_t *src_dev, int m) {
+  const int64_t n_super = (int64_t)F * D / Q8K;
+  k_repack_q8x128<<<(unsigned)((n_super + 255) / 256), 256>>>(src_dev, L->wsh + m * Q8_MAT_BYTES,
+                                                              n_super);
+  HIP_TRY(hipGetLastError());
+  return HY3X_OK;
+}
+
+int hy3x_layer_set_shared_q8_0(hy3x_layer *L, const void *gate, const void *up, const void *down,
+                               int src_on_device) {
+  if (!L || !gate || !up || !down) return fail(HY3X_E_ARG, "NULL argument");
+  int rc = ensure_wsh(L);
+  if (rc) return rc;
+  const void *src[3] = {gate, up, down};
+  uint8_t *stage = nullptr;
+  if (!src_on_device && hipMalloc(&stage, HY3X_Q8_0_MATRIX_BYTES) != hipSuccess)
+    return fail(HY3X_E_NOMEM, "hipMalloc of the Q8_0 staging buffer failed");
+  for (int m = 0; m < 3 && rc == HY3X_OK; m++) {
+    const uint8_t *s = (const uint8_t *)src[m];
+    if (stage) {
+      if (hipMemcpy(stage, s, HY3X_Q8_0_MATRIX_BYTES, hipMemcpyHostToDevice) != hipSuccess) {
+        rc = fail(HY3X_E_HIP, "hipMemcpy of the Q8_0 shared expert failed");
+        break;
+      }
+      s = stage;
+    }
+    rc = repack_q8(L, s, m);
+  }
+  if (rc == HY3X_OK && hipDeviceSynchronize() != hipSuccess)
+    rc = fail(HY3X_E_HIP, "Q8_0 repack failed");
+  if (stage) (void)hipFree(stage);
+  if (rc == HY3X_OK) L->shared_q8 = 1;
+  return rc;
 }
 
 int hy3x_layer_set_path(hy3x_layer *L, int path) {
@@ -238,7 +286,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       if (c.mode == Mode::DECODE) {
         k_route_decode<<<E + DEC_GU_BLOCKS, 256, 0, st>>>(
             x, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
-            L->s16, L->s32, L->wq, L->h16, L->trace[0]);
+            L->s16, L->s32, L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16, L->trace[0]);
         break;
       }
       // the routing kernels also clear (first kernel) and fill (top-K) the
@@ -289,8 +337,8 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
-        k_down_decode<<<D / DEC_DOWN_RPB, 64 * (KMAX + 1), 0, st>>>(L->wq, L->h16, L->ids, L->w,
-                                                                    K, x, L->trace[2]);
+        k_down_decode<<<D / DEC_DOWN_RPB, 64 * (KMAX + 1), 0, st>>>(
+            L->wq, L->h16, L->ids, L->w, K, x, L->shared_q8 ? L->wsh : nullptr, L->trace[2]);
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
         k_moe_mfma<false><<<mt * (D / (32 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->h16m, L->hsum, L->list,
@@ -324,6 +372,8 @@ int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void 
     c.mode = Mode::MFMA;
   else
     c.mode = Mode::GEMV;
+  if (L->shared_q8 && c.mode != Mode::DECODE)
+    return fail(HY3X_E_STATE, "a Q8_0 shared expert is implemented for T = 1 only");
   c.nt = c.mode == Mode::MFMA ? 32 : 4;  // tokens per work tile
   c.mt = std::min(max_tiles_for(T, K, c.nt), L->max_tiles_alloc);
   record_stage(L, st, -1);
@@ -422,6 +472,36 @@ int hy3x_synth_layer_experts(hy3x_layer *L, uint64_t seed, uint32_t layer_index)
   k_synth_q4k<<<(unsigned)((nblocks + 3) / 4), 256>>>(L->wq, nblocks, seed, layer_index, nullptr);
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipDeviceSynchronize());
+  return HY3X_OK;
+}
+
+int hy3x_synth_shared_q8_0(hy3x_layer *L, uint64_t seed, uint32_t layer_index) {
+  if (!L) return fail(HY3X_E_ARG, "NULL layer");
+  int rc = ensure_wsh(L);
+  if (rc) return rc;
+  uint8_t *stage = nullptr;
+  if (hipMalloc(&stage, HY3X_Q8_0_MATRIX_BYTES) != hipSuccess)
+    return fail(HY3X_E_NOMEM, "hipMalloc of the Q8_0 staging buffer failed");
+  const int64_t nblocks = (int64_t)F * D / 32;
+  for (int m = 0; m < 3 && rc == HY3X_OK; m++) {  // kinds gate 5, up 6, down 7; expert 192
+    k_synth_q8_0<<<(unsigned)((nblocks + 255) / 256), 256>>>(
+        stage, nblocks, hy3x_synth_key(seed, layer_index, 5u + m, (uint32_t)E), nullptr);
+    if (hipGetLastError() != hipSuccess) rc = fail(HY3X_E_HIP, "k_synth_q8_0 launch failed");
+    else rc = repack_q8(L, stage, m);
+  }
+  if (rc == HY3X_OK && hipDeviceSynchronize() != hipSuccess)
+    rc = fail(HY3X_E_HIP, "Q8_0 synthesis failed");
+  (void)hipFree(stage);
+  if (rc == HY3X_OK) L->shared_q8 = 1;
+  return rc;
+}
+
+int hy3x_synth_quantize_q8_0(const float *src, void *dst, int64_t n, void *stream) {
+  if (!src || !dst || n <= 0 || n % 32) return fail(HY3X_E_ARG, "bad quantize arguments");
+  const int64_t nblocks = n / 32;
+  k_synth_q8_0<<<(unsigned)((nblocks + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (uint8_t *)dst, nblocks, 0, src);
+  HIP_TRY(hipGetLastError());
   return HY3X_OK;
 }
 

@@ -22,6 +22,7 @@
 // contracted into FMAs beyond the explicit fmaf calls.
 #include "hy3x_route.h"
 #include "hy3x_decode.h"
+#include "hy3x_q8.h"
 
 #pragma clang fp contract(off)
 
@@ -140,7 +141,8 @@ __global__ __launch_bounds__(256) void k_router_logits(
 // Blocks 0..191 compute router logit e (router_block; block 0 also stages s).
 // Blocks 192.. need no routing: they compute s themselves (the same RMSNorm
 // arithmetic as router_block) and stream the shared expert's gate/up rows,
-// 16 per block, into h16 slot K. The top-K runs in the routed gate/up blocks
+// 16 per block, into h16 slot K (wsh != nullptr: the shared expert is the
+// layer's Q8 one, hy3x_q8.h). The top-K runs in the routed gate/up blocks
 // (k_gateup_decode): publishing it from here would need a device-scope
 // release/acquire between blocks, which costs more than recomputing it.
 __global__ __launch_bounds__(256) void k_route_decode(
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(256) void k_route_decode(
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias, int K,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
     __half *__restrict__ s16, float *__restrict__ s32, const uint8_t *__restrict__ wq,
-    __half *__restrict__ h16, unsigned long long *trace) {
+    const uint8_t *__restrict__ wsh, __half *__restrict__ h16, unsigned long long *trace) {
   const int tid = threadIdx.x;
   if (blockIdx.x < E) {
     router_block(blockIdx.x, 0, x, norm_w, router, bias, has_bias, logits, sig, score, s16, s32,
@@ -181,7 +183,10 @@ __global__ __launch_bounds__(256) void k_route_decode(
   float slo, shi;
   group_sums(X, slo, shi);
   trace_point(trace, 1);
-  gateup_rows<DEC_RPW, DEC_RPW>(wq, E, K, sb * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
+  if (wsh)
+    gateup_rows_q8<DEC_RPW, 2>(wsh, K, sb * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
+  else
+    gateup_rows<DEC_RPW, DEC_RPW>(wq, E, K, sb * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
   trace_point(trace, 3);
 }
 

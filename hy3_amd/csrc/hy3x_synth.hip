@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include "hy3x_kernels.h"
+#include "hy3x_q8.h"
 
 #pragma clang fp contract(off)
 
@@ -146,6 +147,60 @@ __global__ __launch_bounds__(256) void k_synth_q4k(uint8_t *dst, int64_t nblocks
     h.z = sc[4] | (sc[5] << 8) | (sc[6] << 16) | ((uint32_t)sc[7] << 24);
     h.w = sc[8] | (sc[9] << 8) | (sc[10] << 16) | ((uint32_t)sc[11] << 24);
     *reinterpret_cast<uint4 *>(blk) = h;
+  }
+}
+
+// hy3 Q8_0 (36-byte blocks, hy3.c:400-403) -> q8x128 super-blocks (hy3x_q8.h):
+// one thread per super-block of 4 source blocks. Source blocks are 4-byte
+// aligned, so everything moves as dwords.
+__global__ __launch_bounds__(256) void k_repack_q8x128(const uint8_t *__restrict__ src,
+                                                       uint8_t *__restrict__ dst,
+                                                       int64_t n_super) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_super) return;
+  const uint32_t *s = reinterpret_cast<const uint32_t *>(src + i * 4 * Q8_BLOCK);
+  uint32_t *o = reinterpret_cast<uint32_t *>(dst + i * QB);
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    o[b] = s[9 * b];
+#pragma unroll
+    for (int w = 0; w < 8; w++) o[4 + 8 * b + w] = s[9 * b + 1 + w];
+  }
+}
+
+// hy3_convert.c:1192-1221 on the device, one thread per 32-weight block:
+// d = amax * (1/127) (the reference build's reciprocal multiply), floored at
+// 1e-10; q = x * (1/d) rounded half away from zero, clamped to +-127. src ==
+// nullptr: the block's values are the synthetic normals of matrix `key`
+// (element index 32 b + k, sigma 0.02); otherwise src[32 b + k].
+__global__ __launch_bounds__(256) void k_synth_q8_0(uint8_t *__restrict__ dst, int64_t nblocks,
+                                                    uint64_t key, const float *__restrict__ src) {
+#pragma clang fp contract(off)
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (b >= nblocks) return;
+  float v[32];
+#pragma unroll
+  for (int k = 0; k < 32; k++)
+    v[k] = src ? src[b * 32 + k] : synth_normal(key, (uint64_t)(b * 32 + k), 0.02f);
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
+  float d = amax * (1.0f / 127.0f);
+  if (d < 1e-10f) d = 1e-10f;
+  const float id = 1.0f / d;
+  uint32_t *o = reinterpret_cast<uint32_t *>(dst + b * Q8_BLOCK);
+  o[0] = __float_as_uint(d);
+#pragma unroll
+  for (int w = 0; w < 8; w++) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float t = v[4 * w + c] * id;
+      int q = (int)(t + (t >= 0.0f ? 0.5f : -0.5f));
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+      word |= (uint32_t)(uint8_t)(int8_t)q << (8 * c);
+    }
+    o[1 + w] = word;
   }
 }
 

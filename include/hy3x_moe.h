@@ -46,6 +46,10 @@ extern "C" {
 #define HY3X_Q4K_BLOCK 144  /* sizeof(block_q4_K) hy3.c:405-410 */
 /* Q4_K bytes of one [1536 x 4096] or [4096 x 1536] matrix. */
 #define HY3X_Q4K_MATRIX_BYTES 3538944
+/* hy3's Q8_0 (f32 d + 32 int8 = 36 bytes per 32 weights, hy3.c:200, 400-403):
+ * bytes of one [1536 x 4096] or [4096 x 1536] matrix. */
+#define HY3X_Q8_0_BLOCK 36
+#define HY3X_Q8_0_MATRIX_BYTES 7077888
 #define HY3X_ROUTE_SCALE 2.826f /* hy3.c:1289, hy3_gpu.cu:717 */
 
 typedef struct hy3x_layer hy3x_layer;
@@ -78,6 +82,20 @@ int hy3x_layer_set_router(hy3x_layer *layer, const float *norm_w, const float *r
  * device pointers. Replaces upload_q4k_compressed (hy3_gpu.cu:515,590). */
 int hy3x_layer_set_expert_q4k(hy3x_layer *layer, int expert, const void *gate, const void *up,
                               const void *down, int src_on_device);
+
+/* The shared expert in hy3's Q8_0, the type real checkpoints carry for
+ * ffn_{gate,up,down}_shexp (hy3_convert.c:684-697 forces it): gate/up
+ * [1536 x 4096], down [4096 x 1536], HY3X_Q8_0_MATRIX_BYTES each, in the
+ * unchanged GGUF block layout (36-byte blocks). Replaces the shared-expert
+ * upload of hy3_gpu_init (hy3_gpu.cu:581-588), which inflates these to F16
+ * (37.7 MB per layer); the layer keeps them as Q8_0 (21.2 MB, repacked into
+ * 144-byte super-blocks of 128 weights on the device) and computes
+ * sum d*q*x like mul_mat_f32 case 8 (hy3.c:1098-1120). From this call on the
+ * forward uses them; hy3x_layer_set_expert_q4k(layer, 192, ...) switches back
+ * to a Q4_K shared expert. Allocates 21.2 MB of device memory on first use.
+ * src_on_device != 0: the pointers are device pointers. */
+int hy3x_layer_set_shared_q8_0(hy3x_layer *layer, const void *gate, const void *up,
+                               const void *down, int src_on_device);
 
 /* Device address of expert e's matrix m (0 gate, 1 up, 2 down) inside the
  * layer's weight arena, for callers that fill the arena directly. */
@@ -143,6 +161,13 @@ int hy3x_layer_set_path(hy3x_layer *layer, int path);
 int hy3x_synth_layer_experts(hy3x_layer *layer, uint64_t seed, uint32_t layer_index);
 /* Quantise n fp32 values (device pointers; n multiple of 256) to Q4_K. */
 int hy3x_synth_quantize_q4k(const float *src, void *dst, int64_t n, void *stream);
+/* The shared expert in hy3's Q8_0 from (seed, layer_index): the same fp32
+ * values as expert 192 of hy3x_synth_layer_experts, quantised by the Q8_0
+ * quantiser of hy3_convert.c:1192-1221 as its Makefile build computes it,
+ * then set as by hy3x_layer_set_shared_q8_0. */
+int hy3x_synth_shared_q8_0(hy3x_layer *layer, uint64_t seed, uint32_t layer_index);
+/* Quantise n fp32 values (device pointers; n multiple of 32) to hy3's Q8_0. */
+int hy3x_synth_quantize_q8_0(const float *src, void *dst, int64_t n, void *stream);
 /* Host-side generators for the small tensors (bit-identical to the spec). */
 uint64_t hy3x_synth_key(uint64_t seed, uint32_t layer, uint32_t kind, uint32_t index);
 void hy3x_synth_normal(float *dst, int64_t n, uint64_t key, uint64_t first, float sigma,

@@ -241,6 +241,53 @@ void hy3o_gen_q4k_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float s
   }
 }
 
+/* hy3_convert.c:1192-1221: d = amax / 127 (the build multiplies by the fp32
+ * reciprocal of 127), floored at 1e-10; q = v rounded half away from zero,
+ * v = x * (1/d), clamped to [-127, 127]; stored as f32 d then 32 int8. */
+static void quantize_block_q8_0(const float *xb, uint8_t *out) {
+  float amax = 0.0f;
+  for (int k = 0; k < 32; k++) {
+    const float a = fabsf(xb[k]);
+    if (a > amax) amax = a;
+  }
+  float d = amax * (1.0f / 127.0f);
+  if (d < 1e-10f) d = 1e-10f;
+  const float id = 1.0f / d;
+  memcpy(out, &d, 4);
+  for (int k = 0; k < 32; k++) {
+    const float v = xb[k] * id;
+    int q = (int)(v + (v >= 0.0f ? 0.5f : -0.5f));
+    if (q > 127) q = 127;
+    if (q < -127) q = -127;
+    out[4 + k] = (uint8_t)(int8_t)q;
+  }
+}
+
+void hy3o_quantize_q8_0(const float *x, uint8_t *dst, int64_t n) {
+  const int64_t nb = n / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < nb; i++) quantize_block_q8_0(x + i * 32, dst + i * HY3O_Q8_BLOCK);
+}
+
+void hy3o_dequant_q8_0(float *dst, const uint8_t *src, int64_t n) {
+  for (int64_t i = 0; i < n / 32; i++) {
+    float d;
+    memcpy(&d, src + i * HY3O_Q8_BLOCK, 4);
+    const int8_t *q = (const int8_t *)(src + i * HY3O_Q8_BLOCK + 4);
+    for (int k = 0; k < 32; k++) dst[i * 32 + k] = d * (float)q[k];
+  }
+}
+
+void hy3o_gen_q8_0_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float sigma) {
+  const int64_t nb = (int64_t)rows * cols / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < nb; b++) {
+    float xb[32];
+    for (int k = 0; k < 32; k++) xb[k] = hy3o_normal(key, (uint64_t)(b * 32 + k), sigma);
+    quantize_block_q8_0(xb, dst + b * HY3O_Q8_BLOCK);
+  }
+}
+
 /* ======================================================================== */
 /* Routing contract                                                          */
 /* ======================================================================== */
@@ -421,6 +468,29 @@ void hy3o_mul_mat_q4k(float *dst, const uint8_t *w, const float *x, int m, int n
   free(tmp);
 }
 
+void hy3o_mul_mat_q8_0(float *dst, const uint8_t *w, const float *x, int m, int n) {
+  const int nb = n / 32;
+#pragma omp parallel for schedule(static)
+  for (int i = 0; i < m; i++) {
+    float sum = 0.0f;
+    const uint8_t *row = w + (size_t)i * nb * HY3O_Q8_BLOCK;
+    for (int j = 0; j < nb; j++) {
+      float d;
+      memcpy(&d, row + (size_t)j * HY3O_Q8_BLOCK, 4);
+      const int8_t *q = (const int8_t *)(row + (size_t)j * HY3O_Q8_BLOCK + 4);
+      for (int l = 0; l < 32; l++) sum += d * (float)q[l] * x[(size_t)j * 32 + l];
+    }
+    dst[i] = sum;
+  }
+}
+
+/* The shared expert's matrices in their own type (index E). */
+static void mul_mat_shared(const hy3o_layer *L, float *dst, const uint8_t *w, const float *x,
+                           int m, int n) {
+  if (L->shared_type == HY3O_TYPE_Q8_0) hy3o_mul_mat_q8_0(dst, w, x, m, n);
+  else hy3o_mul_mat_q4k(dst, w, x, m, n);
+}
+
 static inline float silu_f(float v) { return v / (1.0f + expf(-v)); } /* hy3.c:446-448 */
 
 void hy3o_moe_token(const hy3o_layer *L, float *x, int K, float scale, int32_t *ids,
@@ -431,8 +501,8 @@ void hy3o_moe_token(const hy3o_layer *L, float *x, int K, float scale, int32_t *
   hy3o_route_token(x, L->norm_w, L->router, L->bias, L->bias != NULL, K, scale, s, NULL,
                    NULL, NULL, id, wp, ww);
   /* shared expert (hy3.c:1293-1300) */
-  hy3o_mul_mat_q4k(sh_g, L->gate[HY3O_E], s, HY3O_F, HY3O_D);
-  hy3o_mul_mat_q4k(sh_u, L->up[HY3O_E], s, HY3O_F, HY3O_D);
+  mul_mat_shared(L, sh_g, L->gate[HY3O_E], s, HY3O_F, HY3O_D);
+  mul_mat_shared(L, sh_u, L->up[HY3O_E], s, HY3O_F, HY3O_D);
   for (int i = 0; i < HY3O_F; i++) sh_g[i] = silu_f(sh_g[i]) * sh_u[i];
   /* routed experts (hy3.c:1302-1320) */
   memset(eo, 0, sizeof(eo));
@@ -445,7 +515,7 @@ void hy3o_moe_token(const hy3o_layer *L, float *x, int K, float scale, int32_t *
     for (int i = 0; i < HY3O_D; i++) eo[i] += ww[k] * dn[i];
   }
   /* shared down + residual (hy3.c:1322-1325) */
-  hy3o_mul_mat_q4k(shd, L->down[HY3O_E], sh_g, HY3O_D, HY3O_F);
+  mul_mat_shared(L, shd, L->down[HY3O_E], sh_g, HY3O_D, HY3O_F);
   for (int i = 0; i < HY3O_D; i++) x[i] += shd[i] + eo[i];
   for (int k = 0; k < K; k++) {
     if (ids) ids[k] = id[k];
@@ -489,6 +559,22 @@ static void mul_mat_q4k_f64(double *dst, const uint8_t *w, const double *x, int 
   }
 }
 
+static void mul_mat_q8_0_f64(double *dst, const uint8_t *w, const double *x, int m, int n) {
+  const int nb = n / 32;
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < m; r++) {
+    double acc = 0.0;
+    for (int b = 0; b < nb; b++) {
+      const uint8_t *blk = w + ((size_t)r * nb + b) * HY3O_Q8_BLOCK;
+      float d;
+      memcpy(&d, blk, 4);
+      const int8_t *q = (const int8_t *)(blk + 4);
+      for (int l = 0; l < 32; l++) acc += (double)d * q[l] * x[(size_t)b * 32 + l];
+    }
+    dst[r] = acc;
+  }
+}
+
 void hy3o_moe_token_f64(const hy3o_layer *L, const float *x, double *y, int K, float scale,
                         const int32_t *ids_in) {
   double s[HY3O_D], g[HY3O_F], u[HY3O_F], dn[HY3O_D], acc[HY3O_D];
@@ -509,10 +595,12 @@ void hy3o_moe_token_f64(const hy3o_layer *L, const float *x, double *y, int K, f
   for (int k = 0; k <= K; k++) {
     const int e = k < K ? ids_in[k] : HY3O_E;
     const double wk = k < K ? sg[k] / sum * (double)scale : 1.0;
-    mul_mat_q4k_f64(g, L->gate[e], s, HY3O_F, HY3O_D);
-    mul_mat_q4k_f64(u, L->up[e], s, HY3O_F, HY3O_D);
+    void (*mm)(double *, const uint8_t *, const double *, int, int) =
+        (e == HY3O_E && L->shared_type == HY3O_TYPE_Q8_0) ? mul_mat_q8_0_f64 : mul_mat_q4k_f64;
+    mm(g, L->gate[e], s, HY3O_F, HY3O_D);
+    mm(u, L->up[e], s, HY3O_F, HY3O_D);
     for (int i = 0; i < HY3O_F; i++) g[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
-    mul_mat_q4k_f64(dn, L->down[e], g, HY3O_D, HY3O_F);
+    mm(dn, L->down[e], g, HY3O_D, HY3O_F);
     for (int i = 0; i < HY3O_D; i++) acc[i] += wk * dn[i];
   }
   for (int i = 0; i < HY3O_D; i++) y[i] = x[i] + acc[i];

@@ -31,6 +31,9 @@ extern "C" {
 #define HY3O_KMAX 8          /* n_expert_used default  (hy3.h:40) */
 #define HY3O_QK 256          /* weights per Q4_K super-block */
 #define HY3O_BLOCK_BYTES 144 /* sizeof(block_q4_K)     (hy3.c:405-410) */
+#define HY3O_Q8_BLOCK 36     /* hy3's Q8_0: f32 d + 32 int8 (hy3.c:200, 400-403) */
+#define HY3O_TYPE_Q8_0 8
+#define HY3O_TYPE_Q4_K 12
 #define HY3O_RMS_EPS 1e-5f   /* hy3.c:25 */
 #define HY3O_ROUTE_SCALE 2.826f /* hy3.c:1289 */
 
@@ -67,6 +70,13 @@ void hy3o_dequant_q4k(float *dst, const uint8_t *src, int64_t n);          /* hy
 void hy3o_quantize_q4k(const float *x, uint8_t *dst, int64_t n);           /* hy3_convert.c:605-651 */
 /* Generate an [rows x cols] matrix from the spec and quantise it (OpenMP). */
 void hy3o_gen_q4k_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float sigma);
+/* hy3's Q8_0 (36-byte blocks). The quantiser follows hy3_convert.c:1192-1221
+ * as its Makefile build computes it (amax/127 becomes a multiply by the fp32
+ * reciprocal under -ffast-math); d*q is the block's dequantisation
+ * (hy3.c:1114-1116). */
+void hy3o_quantize_q8_0(const float *x, uint8_t *dst, int64_t n);
+void hy3o_dequant_q8_0(float *dst, const uint8_t *src, int64_t n);
+void hy3o_gen_q8_0_matrix(uint8_t *dst, int rows, int cols, uint64_t key, float sigma);
 
 /* ---- routing contract --------------------------------------------------- */
 /* Fixed-order fp32 dot product (n a multiple of 8): eight fmaf chains over
@@ -98,11 +108,15 @@ typedef struct {
   const uint8_t *gate[HY3O_E + 1]; /* Q4_K [F x D]; index E = shared expert */
   const uint8_t *up[HY3O_E + 1];   /* Q4_K [F x D] */
   const uint8_t *down[HY3O_E + 1]; /* Q4_K [D x F] */
+  int shared_type;                 /* index E: HY3O_TYPE_Q4_K (or 0) or HY3O_TYPE_Q8_0 */
 } hy3o_layer;
 
 /* Q4_K matrix-vector product as the reference computes it: dequantise the whole
  * [m x n] matrix to fp32, then per-row fp32 sums (hy3.c:1122-1135). */
 void hy3o_mul_mat_q4k(float *dst, const uint8_t *w, const float *x, int m, int n);
+/* Q8_0 matrix-vector product (hy3.c:1098-1120): per row, one fp32 sum of
+ * d * q * x over the blocks in order. */
+void hy3o_mul_mat_q8_0(float *dst, const uint8_t *w, const float *x, int m, int n);
 /* One token through the MoE block: x[D] is updated in place (residual).
  * ids/wpre/w (K each) receive the routing when non-NULL. hy3.c:1266-1325. */
 void hy3o_moe_token(const hy3o_layer *L, float *x, int K, float scale,

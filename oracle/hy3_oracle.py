@@ -19,6 +19,9 @@ REF_LIB = os.path.join(HERE, "_ref", "libhy3ref.so")
 D, F, E = 4096, 1536, 192
 QB = 144
 MAT_BYTES = 3538944
+Q8B = 36                      # hy3's Q8_0 block: f32 d + 32 int8
+Q8_MAT_BYTES = F * D // 32 * Q8B
+TYPE_Q8_0, TYPE_Q4_K = 8, 12
 T_X, T_NORM, T_ROUTER, T_BIAS, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7
 
 P = ctypes.c_void_p
@@ -37,6 +40,10 @@ _SIGS = {
     "hy3o_dequant_q4k": (None, [P, P, I64]),
     "hy3o_quantize_q4k": (None, [P, P, I64]),
     "hy3o_gen_q4k_matrix": (None, [P, I32, I32, U64, F32]),
+    "hy3o_quantize_q8_0": (None, [P, P, I64]),
+    "hy3o_dequant_q8_0": (None, [P, P, I64]),
+    "hy3o_gen_q8_0_matrix": (None, [P, I32, I32, U64, F32]),
+    "hy3o_mul_mat_q8_0": (None, [P, P, P, I32, I32]),
     "hy3o_dot8": (F32, [P, P, I32]),
     "hy3o_sig_expf": (F32, [F32]),
     "hy3o_sumsq_block": (F32, [P]),
@@ -59,6 +66,8 @@ _REF_SIGS = {
     "hy3ref_mul_mat": (None, [P, P, U32, P, I32, I32]),
     "hy3ref_set_threads": (None, [I32]),
     "hy3ref_moe_forward": (I32, [P, I32, I32, P, P, P, I32, P, P, P, P, I32]),
+    "hy3ref_moe_forward_t": (I32, [P, I32, I32, P, P, P, I32, P, P, P, P, I32, U32]),
+    "hy3ref_convert": (I32, [ctypes.c_char_p, ctypes.c_char_p, I32]),
     "hy3ref_quantize_q4k": (None, [P, P, I32]),
     "hy3ref_fp32_to_fp16": (ctypes.c_uint16, [F32]),
     "hy3ref_rms_r": (F32, [P, I32]),
@@ -105,7 +114,7 @@ def ptr(a):
 
 class Layer(ctypes.Structure):
     _fields_ = [("norm_w", P), ("router", P), ("bias", P), ("gate", P * (E + 1)),
-                ("up", P * (E + 1)), ("down", P * (E + 1))]
+                ("up", P * (E + 1)), ("down", P * (E + 1)), ("shared_type", I32)]
 
 
 def key(seed, layer, kind, index=0):
@@ -151,12 +160,36 @@ def gen_matrix(seed, layer, kind, expert):
     return out
 
 
+def quantize_q8(x):
+    """hy3's Q8_0 quantiser (hy3_convert.c:1192-1221) on a flat fp32 array."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(x.size // 32 * Q8B, np.uint8)
+    lib().hy3o_quantize_q8_0(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def dequant_q8(q):
+    q = np.ascontiguousarray(q, np.uint8)
+    out = np.empty(q.size // Q8B * 32, np.float32)
+    lib().hy3o_dequant_q8_0(out.ctypes.data, q.ctypes.data, out.size)
+    return out
+
+
+def gen_matrix_q8(seed, layer, kind, expert):
+    """The same fp32 values as gen_matrix, quantised to hy3's Q8_0."""
+    rows, cols = (D, F) if kind == T_DOWN else (F, D)
+    out = np.empty(Q8_MAT_BYTES, np.uint8)
+    lib().hy3o_gen_q8_0_matrix(out.ctypes.data, rows, cols, key(seed, layer, kind, expert), 0.02)
+    return out
+
+
 class SynthLayer:
     """CPU copy of a synthetic layer; expert matrices are generated lazily
     (or supplied, e.g. copied back from the device)."""
 
-    def __init__(self, weight_seed, layer=0, zipf_seed=None, has_bias=True):
+    def __init__(self, weight_seed, layer=0, zipf_seed=None, has_bias=True, shared_q8=False):
         self.seed, self.layer = weight_seed, layer
+        self.shared_q8 = shared_q8  # shared expert in hy3's Q8_0 (real checkpoints)
         self.norm_w = normal(D, key(weight_seed, layer, T_NORM), 0.02, 1.0)
         self.router = normal(E * D, key(weight_seed, layer, T_ROUTER), 0.02)
         if zipf_seed is not None:
@@ -168,7 +201,8 @@ class SynthLayer:
 
     def expert(self, e):
         if e not in self.experts:
-            self.experts[e] = tuple(gen_matrix(self.seed, self.layer, k, e)
+            gen = gen_matrix_q8 if (e == E and self.shared_q8) else gen_matrix
+            self.experts[e] = tuple(gen(self.seed, self.layer, k, e)
                                     for k in (T_GATE, T_UP, T_DOWN))
         return self.experts[e]
 
@@ -180,6 +214,7 @@ class SynthLayer:
         s.bias = self.bias.ctypes.data if self.has_bias else None
         for e, (g, u, d) in self.experts.items():
             s.gate[e], s.up[e], s.down[e] = g.ctypes.data, u.ctypes.data, d.ctypes.data
+        s.shared_type = TYPE_Q8_0 if self.shared_q8 else TYPE_Q4_K
         return s
 
     def route(self, x, K=8, scale=2.826, r_override=None):
@@ -240,9 +275,10 @@ class SynthLayer:
         scores = np.zeros((T, E), np.float32)
         ptrs = [(P * (E + 1))(*[self.experts[e][m].ctypes.data for e in range(E + 1)])
                 for m in range(3)]
-        R.hy3ref_moe_forward(y.ctypes.data, T, K, self.norm_w.ctypes.data, self.router.ctypes.data,
-                             self.bias.ctypes.data, 1 if self.has_bias else 0, ptrs[0], ptrs[1],
-                             ptrs[2], scores.ctypes.data, 1)
+        R.hy3ref_moe_forward_t(y.ctypes.data, T, K, self.norm_w.ctypes.data,
+                               self.router.ctypes.data, self.bias.ctypes.data,
+                               1 if self.has_bias else 0, ptrs[0], ptrs[1], ptrs[2],
+                               scores.ctypes.data, 1, TYPE_Q8_0 if self.shared_q8 else TYPE_Q4_K)
         return y, scores
 
 

@@ -60,12 +60,17 @@ static hy3_tensor_info ti_f32 = {0}, ti_q4k = {0}, ti_none = {0};
 /* x: [T x 4096] updated in place. gate/up/down: 193 host pointers each (index
  * 192 = shared expert). scores_out: [T x 192] or NULL. quiet: silence the
  * attention half's "unsupported ggml_type" diagnostics. Returns 0. */
-int hy3ref_moe_forward(float *x, int T, int K, const float *norm_w, const float *router,
-                       const float *bias, int has_bias, const uint8_t *const *gate,
-                       const uint8_t *const *up, const uint8_t *const *down,
-                       float *scores_out, int quiet) {
+static hy3_tensor_info ti_shared = {0};
+
+/* shared_type: the shared expert's ggml type (12 Q4_K, or 8 for hy3's Q8_0,
+ * the type hy3_convert.c:684-697 forces for ffn_*_shexp). */
+int hy3ref_moe_forward_t(float *x, int T, int K, const float *norm_w, const float *router,
+                         const float *bias, int has_bias, const uint8_t *const *gate,
+                         const uint8_t *const *up, const uint8_t *const *down,
+                         float *scores_out, int quiet, uint32_t shared_type) {
   ti_f32.ggml_type = 0;
   ti_q4k.ggml_type = 12;
+  ti_shared.ggml_type = shared_type;
   ti_none.ggml_type = 0x7fffffff;
   hy3_model *m = (hy3_model *)calloc(1, sizeof(hy3_model));
   static float ones[HY3_N_EMBD];
@@ -91,9 +96,9 @@ int hy3ref_moe_forward(float *x, int T, int K, const float *norm_w, const float 
     l->expert_bias[e] = has_bias ? bias[e] : 0.0f;
   }
   l->has_expert_bias = has_bias ? true : false;
-  l->ffn_gate_shexp.t = &ti_q4k; l->ffn_gate_shexp.data = gate[HY3_N_EXPERT];
-  l->ffn_up_shexp.t = &ti_q4k; l->ffn_up_shexp.data = up[HY3_N_EXPERT];
-  l->ffn_down_shexp.t = &ti_q4k; l->ffn_down_shexp.data = down[HY3_N_EXPERT];
+  l->ffn_gate_shexp.t = &ti_shared; l->ffn_gate_shexp.data = gate[HY3_N_EXPERT];
+  l->ffn_up_shexp.t = &ti_shared; l->ffn_up_shexp.data = up[HY3_N_EXPERT];
+  l->ffn_down_shexp.t = &ti_shared; l->ffn_down_shexp.data = down[HY3_N_EXPERT];
 
   int saved = -1;
   if (quiet) {
@@ -111,4 +116,12 @@ int hy3ref_moe_forward(float *x, int T, int K, const float *norm_w, const float 
   if (quiet && saved >= 0) { fflush(stderr); dup2(saved, 2); close(saved); }
   free(m->scratch); free(m->scratch2); free(m->cache_k); free(m->cache_v); free(m);
   return 0;
+}
+
+int hy3ref_moe_forward(float *x, int T, int K, const float *norm_w, const float *router,
+                       const float *bias, int has_bias, const uint8_t *const *gate,
+                       const uint8_t *const *up, const uint8_t *const *down,
+                       float *scores_out, int quiet) {
+  return hy3ref_moe_forward_t(x, T, K, norm_w, router, bias, has_bias, gate, up, down,
+                              scores_out, quiet, 12);
 }

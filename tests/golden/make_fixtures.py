@@ -15,11 +15,19 @@ Runs ONLY in a container that holds the reference sources at /root/reference
                     (sigmoid+bias), selected ids, sigmoid bits, output rows, and the
                     build's RMSNorm scale r per token (rsqrt estimate + Newton step,
                     host-CPU dependent), checked to reproduce forward_layer_moe's scores
+  q8_quant.npz      hy3_convert.c's Q8_0 quantiser (:1192-1221, inline in the converter):
+                    the converter run on a one-tensor safetensors directory holding edge
+                    and random blocks as a shared-expert matrix (:684-697 force Q8_0),
+                    and the Q8_0 bytes read back from the GGUF it writes
+  moe_q8.npz        forward_layer_moe with the shared expert in hy3's Q8_0 (the type real
+                    checkpoints carry), on config-0/1 tokens
 
-Usage: python tests/golden/make_fixtures.py   (about 2 minutes on 8 cores)
+Usage: python tests/golden/make_fixtures.py [--only q8]   (all: about 2 minutes on 8 cores)
 """
+import argparse
 import hashlib
 import json
+import tempfile
 import os
 import platform
 import subprocess
@@ -30,6 +38,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 from oracle import hy3_oracle as O  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
@@ -41,11 +50,77 @@ def sha(a):
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
 
+def write_safetensors_dir(d, tensors):
+    """model.safetensors.index.json + one F32 shard, the input hy3_convert reads
+    (st_db_open, hy3_convert.c:246-410)."""
+    header, blobs, off = {}, [], 0
+    for name, a in tensors.items():
+        a = np.ascontiguousarray(a, np.float32)
+        header[name] = {"dtype": "F32", "shape": list(a.shape), "data_offsets": [off, off + a.nbytes]}
+        blobs.append(a.tobytes())
+        off += a.nbytes
+    hj = json.dumps(header).encode()
+    hj += b" " * (-len(hj) % 8)
+    shard = "model-00001-of-00001.safetensors"
+    with open(os.path.join(d, shard), "wb") as f:
+        f.write(len(hj).to_bytes(8, "little") + hj + b"".join(blobs))
+    with open(os.path.join(d, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {}, "weight_map": {n: shard for n in tensors}}, f)
+
+
+def q8_fixtures(R, lay_seed=0xC0):
+    from gguf_read import Reader
+    rng = np.random.default_rng(8)
+    rows = []
+    rows.append(np.zeros(256))
+    rows.append(np.full(256, 0.5))
+    rows.append(np.linspace(-1, 1, 256))
+    r = np.arange(256) % 32 - 15.5; rows.append(r / 127.0 * 3.0)  # many exact halves of d
+    rows.append(rng.standard_normal(256) * 1e-12)  # d floored at 1e-10
+    rows.append(rng.standard_normal(256) * 1e4)
+    r = rng.standard_normal(256) * 0.02; r[::32] = 0.5; rows.append(r)  # amax element -> 127
+    r = rng.standard_normal(256) * 0.02; r[5::32] = -0.75; rows.append(r)  # negative amax -> -127
+    r = np.round(rng.standard_normal(256) * 16) / 8; rows.append(r)
+    for _ in range(23):
+        rows.append(rng.standard_normal(256) * 0.02)
+    x = np.stack(rows).astype(np.float32)  # [32 x 256]
+    with tempfile.TemporaryDirectory() as d:
+        write_safetensors_dir(d, {"model.layers.1.mlp.shared_mlp.gate_proj.weight": x})
+        out = os.path.join(d, "q8.gguf")
+        assert R.hy3ref_convert(d.encode(), out.encode(), 8) == 0
+        g = Reader(out)
+        q, dims, ty = g.tensor_bytes("blk.1.ffn_gate_shexp.weight")
+    assert ty == 8 and q.size == x.size // 32 * 36, (ty, q.size)
+    mine = O.quantize_q8(x.ravel())
+    print(f"q8 quantiser: oracle-vs-reference byte mismatches {int((mine != q).sum())}", flush=True)
+    np.savez_compressed(os.path.join(OUT, "q8_quant.npz"), x=x, q=q, dims=np.array(dims))
+
+    # MoE block with a Q8_0 shared expert (every routed expert as in layer.json)
+    lay = O.SynthLayer(lay_seed, shared_q8=True)
+    fx = {}
+    R.hy3ref_set_threads(os.cpu_count())
+    for name, seed, nt in (("c0", 0xC0, 1), ("c1", 0xC1, 3)):
+        x = O.normal(nt * D, O.key(seed, 0, O.T_X), 1.0).reshape(nt, D)
+        y, scores = lay.ref_forward(x, 8)
+        fx[f"{name}/x_seed"] = np.array([seed], np.int64)
+        fx[f"{name}/scores"] = scores
+        fx[f"{name}/y"] = y
+        print(f"q8 case {name} done", flush=True)
+    fx["shared_sha256"] = np.array([sha(m) for m in lay.expert(E)])
+    np.savez_compressed(os.path.join(OUT, "moe_q8.npz"), **fx)
+
+
 def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", choices=["q8"], default=None)
+    a = ap.parse_args()
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref", f"REF={REF}"],
                    check=True)
     R = O.ref_lib()
     assert R is not None
+    if a.only == "q8":
+        q8_fixtures(R)
+        return
     meta = {
         "reference": REF,
         "compiler": subprocess.run(["gcc", "--version"], capture_output=True,
@@ -208,6 +283,7 @@ def main():
         print(f"case {name} done", flush=True)
     lay.bias = uni_bias
     np.savez_compressed(os.path.join(OUT, "moe.npz"), **fx)
+    q8_fixtures(R)
     print("all fixtures written", flush=True)
 
 

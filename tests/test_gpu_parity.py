@@ -327,3 +327,71 @@ def test_graph_replay_matches_eager(torch, layer, T):
         ot = other.clone()  # an eager forward on another buffer between replays
         layer.forward(ot.data_ptr(), T, 8)
         torch.cuda.synchronize()
+
+
+# ------------------------------------------------------- hy3 Q8_0 shared expert
+def test_q8_quantiser_matches_oracle(torch):
+    """The device Q8_0 quantiser reproduces the oracle's bytes, which reproduce
+    the reference converter's (tests/golden/q8_quant.npz)."""
+    f = np.load(os.path.join(G, "q8_quant.npz"))
+    x = torch.from_numpy(f["x"].ravel().copy()).cuda()
+    out = torch.zeros(x.numel() // 32 * 36, dtype=torch.uint8, device="cuda")
+    H._check(H.lib().hy3x_synth_quantize_q8_0(x.data_ptr(), out.data_ptr(), x.numel(), None))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), f["q"])
+
+
+@pytest.fixture(scope="module")
+def q8_mats():
+    return tuple(O.gen_matrix_q8(C.WEIGHT_SEED, 0, k, E) for k in (O.T_GATE, O.T_UP, O.T_DOWN))
+
+
+def q8_oracle(cpu, q8_mats, ids):
+    """Oracle layer: the device's routed experts, the Q8_0 shared expert."""
+    o = O.SynthLayer(C.WEIGHT_SEED, shared_q8=True)
+    o.bias, o.has_bias = cpu.bias, cpu.has_bias
+    for e in np.unique(ids):
+        o.experts[int(e)] = cpu.expert(int(e))
+    o.experts[E] = q8_mats
+    return o
+
+
+@pytest.fixture
+def q8_layer(layer, cpu, q8_mats):
+    set_bias(layer, cpu, "uniform")
+    layer.set_shared_q8_0(*q8_mats)
+    yield layer
+    layer.set_expert_q4k(E, *cpu.expert(E))  # back to the Q4_K shared expert
+
+
+def test_q8_shared_decode_matches_oracle_and_reference(torch, q8_layer, cpu, q8_mats):
+    """T = 1 with hy3's Q8_0 shared expert: routing bit-exact, output within
+    TOL of the oracle and of hy3.c's forward_layer_moe (moe_q8.npz)."""
+    f = np.load(os.path.join(G, "moe_q8.npz"))
+    x = O.normal(D, O.key(0xC0, 0, O.T_X), 1.0).reshape(1, D)
+    y, ids, wpre, w = run(torch, q8_layer, x)
+    yo, ro = q8_oracle(cpu, q8_mats, ids).forward(x)
+    assert np.array_equal(ids, ro["ids"])
+    assert np.array_equal(wpre.view(np.uint32), ro["wpre"].view(np.uint32))
+    assert O.rel_l2(y - x, yo - x) <= TOL
+    assert O.rel_l2(y - x, f["c0/y"] - x) <= TOL
+    assert O.rel_l2(y, f["c0/y"]) <= TOL
+
+
+def test_q8_shared_synth_equals_upload(torch, q8_layer):
+    """hy3x_synth_shared_q8_0 (device generator + quantiser) gives the layer the
+    same bytes as uploading the oracle's: identical outputs."""
+    x = O.normal(D, O.key(0xC0, 0, O.T_X), 1.0).reshape(1, D)
+    y1 = run(torch, q8_layer, x)[0]
+    q8_layer.synth_shared_q8_0(C.WEIGHT_SEED, 0)
+    y2 = run(torch, q8_layer, x)[0]
+    assert np.array_equal(y1, y2)
+
+
+def test_q4k_shared_restored_after_q8(torch, layer, cpu):
+    """Setting expert 192 in Q4_K switches the layer back from the Q8 shared expert."""
+    set_bias(layer, cpu, "uniform")
+    x = O.normal(D, O.key(0xC0, 0, O.T_X), 1.0).reshape(1, D)
+    y, ids, _, _ = run(torch, layer, x)
+    yo, _ = cpu.forward(x)
+    assert O.rel_l2(y - x, yo - x) <= TOL

@@ -256,3 +256,78 @@ def test_block_output_matches_reference(moe, base_layer, name):
     assert np.array_equal(r["ids"], moe[f"{name}/ids"][:T])
     assert O.rel_l2(y - x, y_ref - x) < 1e-5
     assert O.rel_l2(y, y_ref) < 1e-5
+
+
+# ------------------------------------------------------------ hy3 Q8_0 (shared)
+def test_q8_quantizer_matches_reference():
+    """hy3_convert.c's Q8_0 quantiser (inline in the converter, :1192-1221) as the
+    reference build computes it: the fixture holds the bytes its converter wrote
+    for edge and random blocks; the restatement reproduces every byte. 14 of the
+    fixture's 256 blocks have an amax for which amax*(1/127) and amax/127 round
+    differently, so the fast-math reciprocal form is pinned too."""
+    f = load("q8_quant.npz")
+    assert np.array_equal(O.quantize_q8(f["x"].ravel()), f["q"])
+    amax = np.abs(f["x"].reshape(-1, 32)).max(1).astype(np.float32)
+    assert np.sum(amax * np.float32(1.0 / 127.0) != amax / np.float32(127.0)) > 0
+
+
+def test_q8_quant_properties():
+    """Closed-form facts of the quantiser: |q| <= 127; the block's largest |x|
+    maps to +-127 when d is not floored; |x - d q| <= d/2 (plus rounding of
+    x/d); d >= 1e-10."""
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(32 * 64) * 0.02, rng.standard_normal(32 * 4) * 1e-13,
+                        np.zeros(32)]).astype(np.float32)
+    q = O.quantize_q8(x)
+    blk = q.reshape(-1, 36)
+    d = blk[:, :4].copy().view(np.float32)[:, 0]
+    qs = blk[:, 4:].view(np.int8).astype(np.int32)
+    xb = x.reshape(-1, 32)
+    assert np.all(np.abs(qs) <= 127) and np.all(d >= np.float32(1e-10))
+    big = d > 1e-10
+    assert np.all(np.abs(qs[big]).max(1) == 127)
+    err = np.abs(xb - d[:, None] * qs)
+    assert np.all(err <= d[:, None] * 0.5 * (1 + 1e-5) + 1e-30)
+    np.testing.assert_array_equal(O.dequant_q8(q), (d[:, None] * qs).astype(np.float32).ravel())
+
+
+def test_q8_matvec_vs_fp64():
+    """hy3.c:1098-1120 (one fp32 sum per row of d*q*x) against an fp64 brute
+    force over the dequantised weights."""
+    rng = np.random.default_rng(4)
+    m, n = 48, 512
+    w = O.quantize_q8((rng.standard_normal(m * n) * 0.02).astype(np.float32))
+    x = rng.standard_normal(n).astype(np.float32)
+    out = np.zeros(m, np.float32)
+    O.lib().hy3o_mul_mat_q8_0(out.ctypes.data, w.ctypes.data, x.ctypes.data, m, n)
+    ref = O.dequant_q8(w).reshape(m, n).astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+    # a single nonzero weight picks out d * q * x exactly
+    w2 = np.zeros(36 * (n // 32), np.uint8)
+    w2[0:4] = np.frombuffer(np.float32(0.25).tobytes(), np.uint8)
+    w2[4 + 7] = np.uint8(np.int8(-3).view(np.uint8))
+    o2 = np.zeros(1, np.float32)
+    O.lib().hy3o_mul_mat_q8_0(o2.ctypes.data, w2.ctypes.data, x.ctypes.data, 1, n)
+    assert o2[0] == np.float32(0.25 * -3.0) * x[7]
+
+
+@pytest.fixture(scope="module")
+def q8_layer():
+    return O.SynthLayer(0xC0, shared_q8=True)
+
+
+def test_q8_shared_bytes_match_fixture(q8_layer):
+    ref = [str(s) for s in load("moe_q8.npz")["shared_sha256"]]
+    assert [sha(m) for m in q8_layer.expert(E)] == ref
+
+
+@pytest.mark.parametrize("name", ["c0", "c1"])
+def test_q8_block_output_matches_reference(q8_layer, name):
+    """forward_layer_moe with hy3's Q8_0 shared expert (hy3.c:1293-1300,
+    1322-1323 through mul_mat_f32 case 8): the oracle's block output."""
+    f = load("moe_q8.npz")
+    y_ref = f[f"{name}/y"]
+    T = y_ref.shape[0]
+    x = O.normal(T * D, O.key(int(f[f"{name}/x_seed"][0]), 0, O.T_X), 1.0).reshape(T, D)
+    y, _ = q8_layer.forward(x, 8)
+    assert O.rel_l2(y - x, y_ref - x) < 1e-5
