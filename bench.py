@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0
 PEAK_F16_TFLOPS = 2500.0
 MAT = 3538944
+Q8MAT = 7077888  # one matrix in hy3's Q8_0 (the shared expert of real checkpoints)
 
 
 def parse():
@@ -45,6 +46,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--path", type=int, default=0, choices=(0, 1, 2),
                    help="expert path: 0 the library's choice by T, 1 GEMV tiles, 2 MFMA tiles")
+    p.add_argument("--shared-q8", action="store_true",
+                   help="shared expert in hy3's Q8_0, the type real checkpoints carry "
+                        "(the configs' default is Q4_K)")
     p.add_argument("--graph", action="store_true",
                    help="replay a HIP graph of each step's kernels instead of launching them "
                         "directly (measured slower than direct launches on ROCm 7.2)")
@@ -86,23 +90,25 @@ def default_steps(T, n_layers):
     return {1: 2000, 32: 500}.get(T, 50 if T <= 512 else 10)
 
 
-def stage_bytes(stage, U, T, K, decode):
+def stage_bytes(stage, U, T, K, decode, shared_q8=False):
     """Algorithmic HBM bytes of one launch of a kernel stage. Single-token
     decode: the router stage also streams the shared expert's gate/up and the
-    gate/up stage streams the K routed experts only."""
+    gate/up stage streams the K routed experts only. shared_q8: the shared
+    expert's matrices are hy3 Q8_0 (Q8MAT bytes each)."""
+    sh = Q8MAT if shared_q8 else MAT
     router = 192 * 4096 * 4 + 4096 * 4 + T * 4096 * 4 + T * 4096 * 6
     if decode:
         if stage == "gateup":
             return K * 2 * MAT + 4096 * 2 + K * 1536 * 2
         if stage == "down":
-            return (K + 1) * MAT + (K + 1) * 1536 * 2 + 2 * 4096 * 4
+            return K * MAT + sh + (K + 1) * 1536 * 2 + 2 * 4096 * 4
         if stage == "router":
-            return router + 2 * MAT + 1536 * 2
+            return router + 2 * sh + 1536 * 2
         return 0
     if stage == "gateup":
-        return U * 2 * MAT + T * 4096 * 2 + T * (K + 1) * 1536 * 2
+        return (U - 1) * 2 * MAT + 2 * sh + T * 4096 * 2 + T * (K + 1) * 1536 * 2
     if stage == "down":
-        return U * MAT + T * (K + 1) * (1536 * 2 + 4096 * 4)
+        return (U - 1) * MAT + sh + T * (K + 1) * (1536 * 2 + 4096 * 4)
     if stage == "router":
         return router
     return 0
@@ -118,11 +124,13 @@ def dominant_kernel(stage, T, path):
     return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
 
 
-def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0):
+def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=False):
     layers = []
     for li in range(cfg.n_layers):
         L = H.MoELayer(cfg.T)
         L.synth_experts(cfg.weight_seed, li)
+        if shared_q8:
+            L.synth_shared_q8_0(cfg.weight_seed, li)
         nw, rt, b = C.config_tensors(cfg, li)
         L.set_router(nw, rt, b)
         if path:
@@ -182,13 +190,13 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0):
     dom = max(("gateup", "down"), key=lambda k: stage_us[k])
     kernel = dominant_kernel(dom, cfg.T, layers[0].path)
     decode = cfg.T == 1 and layers[0].path == 0
-    dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K, decode)
+    dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K, decode, shared_q8)
     # launch duration of the dominant kernel: replayed back to back on the launch
     # stream between two HIP events, after the timed forwards
     reps = max(10, min(steps, 2000))
     launch_us = layers[-1].time_stage(dom, reps, stream=stream)
     achieved = dom_bytes / (launch_us * 1e-6) / 1e9
-    alg_bytes = C.algorithmic_bytes(cfg.T, U) * cfg.n_layers
+    alg_bytes = (C.algorithmic_bytes(cfg.T, U) + (3 * (Q8MAT - MAT) if shared_q8 else 0)) * cfg.n_layers
     flops = C.algorithmic_flops(cfg.T, cfg.K) * cfg.n_layers
     for L in layers:
         L.close()
@@ -203,15 +211,16 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0):
     )
 
 
-def cpu_baseline(torch, H, C, cfg, seconds):
-    """hy3.c's CPU MoE block on a bounded token sample (same Q4_K bytes)."""
+def cpu_baseline(torch, H, C, cfg, seconds, shared_q8=False):
+    """hy3.c's CPU MoE block on a bounded token sample (same Q4_K bytes; with
+    shared_q8 the same Q8_0 shared expert)."""
     from oracle import hy3_oracle as O
     from hy3_amd import hipmem
     L = H.MoELayer(1)
     L.synth_experts(cfg.weight_seed, 0)
     lay = O.SynthLayer(cfg.weight_seed, 0,
-                       zipf_seed=cfg.input_seed if cfg.zipf_bias else None)
-    for e in range(193):
+                       zipf_seed=cfg.input_seed if cfg.zipf_bias else None, shared_q8=shared_q8)
+    for e in range(193 if not shared_q8 else 192):
         lay.experts[e] = tuple(hipmem.to_host(L.expert_ptr(e, m), MAT) for m in range(3))
     L.close()
     ref = O.ref_lib()
@@ -253,7 +262,8 @@ def main():
     torch.cuda.init()
     cfg = C.CONFIGS[a.config]
     steps = a.steps or default_steps(cfg.T, cfg.n_layers)
-    r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph, path=a.path)
+    r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph, path=a.path,
+                shared_q8=a.shared_q8)
     out = {
         "metric": "MoE-layer tokens/s (decode B=1) and achieved HBM GB/s vs peak",
         "value": round(r["tokens_per_s"], 2),
@@ -267,7 +277,8 @@ def main():
                    "layers": cfg.n_layers, "top_k": cfg.K, "experts": "192+1 shared",
                    "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu",
                    "launch": "hip-graph" if a.graph else "direct",
-                   "expert_path": ["auto", "gemv", "mfma"][a.path]},
+                   "expert_path": ["auto", "gemv", "mfma"][a.path],
+                   "shared_expert": "q8_0" if a.shared_q8 else "q4_k"},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),
                   "hbm_frac": round(r["layer_GBps"] / PEAK_HBM_GBS, 4),
                   "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},
@@ -279,7 +290,7 @@ def main():
             if c.index == cfg.index:
                 continue
             rr = measure(torch, H, C, c, default_steps(c.T, c.n_layers), 3,
-                         use_graph=a.graph)
+                         use_graph=a.graph, shared_q8=a.shared_q8)
             sec[f"config{c.index}:{c.name}"] = {
                 "tokens_per_s": round(rr["tokens_per_s"], 1),
                 "ms_per_step": round(rr["ms_per_step"], 4),
@@ -290,7 +301,7 @@ def main():
             torch.cuda.empty_cache()
         out["secondary"] = sec
     if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(torch, H, C, cfg, a.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(torch, H, C, cfg, a.cpu_seconds, a.shared_q8)
     print(json.dumps(out), flush=True)
 
 

@@ -67,12 +67,14 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
 constexpr int MFMA_WAVES = HY3X_MFMA_WAVES;
 template <bool GATEUP>
 __global__ __launch_bounds__(64 * MFMA_WAVES) void k_moe_mfma(
-    const uint8_t *wq, const __half *act, const __half *act_sum, const int32_t *list,
-    const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m, float *out);
-extern template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const __half *,
-                                                 const int32_t *, const int4 *, const int32_t *,
-                                                 int, int, __half *, float *);
-extern template __global__ void k_moe_mfma<false>(const uint8_t *, const __half *, const __half *,
+    const uint8_t *wq, const uint8_t *wsh, const __half *act, const __half *act_sum,
+    const int32_t *list, const int4 *tiles, const int32_t *n_tiles, int T, int K,
+    __half *h16m, float *out);
+extern template __global__ void k_moe_mfma<true>(const uint8_t *, const uint8_t *, const __half *,
+                                                 const __half *, const int32_t *, const int4 *,
+                                                 const int32_t *, int, int, __half *, float *);
+extern template __global__ void k_moe_mfma<false>(const uint8_t *, const uint8_t *,
+                                                  const __half *, const __half *,
                                                   const int32_t *, const int4 *, const int32_t *,
                                                   int, int, __half *, float *);
 __global__ void k_stage_mfma(const float *s32, __half *s16m, __half *ssum);

@@ -328,7 +328,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                           c.scale, L->ids, L->wpre, L->w,
                                                           L->stats, L->h16, L->trace[1]);
       else if (c.mode == Mode::MFMA)
-        k_moe_mfma<true><<<mt * (F / (16 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->s16m, L->ssum, L->list,
+        k_moe_mfma<true><<<mt * (F / (16 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list,
                                                         L->tiles, L->n_tiles, T, K, L->h16m,
                                                         nullptr);
       else
@@ -341,7 +341,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
             L->wq, L->h16, L->ids, L->w, K, x, L->shared_q8 ? L->wsh : nullptr, L->trace[2]);
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
-        k_moe_mfma<false><<<mt * (D / (32 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->h16m, L->hsum, L->list,
+        k_moe_mfma<false><<<mt * (D / (32 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16m, L->hsum, L->list,
                                                           L->tiles, L->n_tiles, T, K, nullptr,
                                                           L->out);
       }
@@ -372,8 +372,8 @@ int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void 
     c.mode = Mode::MFMA;
   else
     c.mode = Mode::GEMV;
-  if (L->shared_q8 && c.mode != Mode::DECODE)
-    return fail(HY3X_E_STATE, "a Q8_0 shared expert is implemented for T = 1 only");
+  if (L->shared_q8 && c.mode == Mode::GEMV)
+    return fail(HY3X_E_STATE, "the GEMV tile path needs a Q4_K shared expert");
   c.nt = c.mode == Mode::MFMA ? 32 : 4;  // tokens per work tile
   c.mt = std::min(max_tiles_for(T, K, c.nt), L->max_tiles_alloc);
   record_stage(L, st, -1);

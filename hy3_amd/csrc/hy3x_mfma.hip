@@ -40,6 +40,7 @@
 #include "hy3x_kernels.h"
 #include "hy3x_q4k.h"
 #include "hy3x_dma.h"
+#include "hy3x_q8.h"
 
 namespace hy3x {
 
@@ -198,8 +199,8 @@ __device__ __forceinline__ void issue_b(const TileState<GATEUP, NTT> &st, int kb
     dma16_s(st.sbase + (size_t)kb * 64, st.soff,
             lds_addr(&bm_st[buf][0][0] + S_LANES * wave));
 }
-template <bool GATEUP, int NTT>
-__device__ __forceinline__ void issue_a(const TileState<GATEUP, NTT> &st, int ka) {
+template <class State>  // TileState or TileStateQ8: the weight copies are the same
+__device__ __forceinline__ void issue_a(const State &st, int ka) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const u4_t *dst = &a_ring[ka % A_STAGES][0] + A_CHUNKS_WAVE * wave;
   const uint8_t *ab = st.abase + (size_t)ka * QB;
@@ -316,6 +317,35 @@ __device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
     }
 }
 
+// Epilogue: lane holds D[token 16t + 4g + i][row] for its own weight row.
+// GATEUP: h = silu(gate) * up -> h16m[slot][perm8(row)]; else out[slot][row].
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void store_tile(
+    const f4_t (&acc)[MfmaCfg<GATEUP>::RG][MfmaCfg<GATEUP>::NMAT][NTT], int n, int rt,
+    __half *__restrict__ h16m, float *__restrict__ out) {
+  using C = MfmaCfg<GATEUP>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int rg = 0; rg < C::RG; rg++) {
+    const int r = rt * C::TROWS + 16 * (GATEUP ? wave : 2 * wave + rg) + lr;
+#pragma unroll
+    for (int t = 0; t < NTT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int tok = 16 * t + 4 * g + i;
+        if (tok < n) {
+          const int slot = t_slot[tok];
+          if constexpr (GATEUP) {
+            h16m[(size_t)slot * F + perm8(r)] =
+                __float2half(silu(acc[rg][0][t][i]) * acc[rg][1][t][i]);
+          } else {
+            out[(size_t)slot * D + r] = acc[rg][0][t][i];
+          }
+        }
+      }
+  }
+}
+
 // One work tile with NTT token tiles of 16 (n <= 16 * NTT tokens).
 template <bool GATEUP, int NTT>
 __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
@@ -379,26 +409,152 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
   // drain the trailing re-copies before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // epilogue: lane holds D[token 16t + 4g + i][row] for its own weight row
+  store_tile<GATEUP, NTT>(st.acc, n, rt, h16m, out);
+}
+
+// ---------------------------------------------------------------------------
+// The shared expert in Q8 (q8x128 super-blocks, hy3x_q8.h). A column is one
+// 144-byte super-block per row = 128 k = four 32-weight blocks, each exactly
+// one 16x16x32 MFMA, so the weight copies are the Q4_K path's (issue_a).
+// Activations: 16 chunks per token per column in bt_st[buf] viewed as
+// [32 tokens][16 chunks], chunk c of row r at position c ^ (r & 15). The
+// weights are the exact integers q in fp16 ((1152 + q) from the byte
+// permute, minus 1152) and each block's MFMA result is scaled by its d in
+// fp32: acc += d_b * (x_b . q_b) -- sum d*q*x as mul_mat_f32 case 8
+// (hy3.c:1098-1120).
+constexpr int B8_DMA = MT_TOK * 16 / 64 / MT_WAVES;  // activation copies per wave
+
+template <bool GATEUP, int NTT>
+struct TileStateQ8 {
+  using C = MfmaCfg<GATEUP>;
+  static constexpr int RG = C::RG, NMAT = C::NMAT, NKB = C::KD / Q8K;
+  const uint8_t *abase;   // the shared expert's Q8 matrices (uniform)
+  uint32_t aoff[A_DMA];   // weight chunks, from abase
+  bool a_last;            // the half-used last weight copy is active in this lane
+  const uint8_t *bbase;   // activations (uniform)
+  uint32_t boff[B8_DMA];  // activation chunks, from bbase
+  f4_t acc[RG][NMAT][NTT];
+};
+
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void issue_b_q8(const TileStateQ8<GATEUP, NTT> &st, int kb) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const u4_t *dst = &bt_st[kb & 1][0][0];
+  const uint8_t *bb = st.bbase + (size_t)kb * Q8K * 2;
 #pragma unroll
-  for (int rg = 0; rg < RG; rg++) {
-    const int r = rt * C::TROWS + 16 * (GATEUP ? wave : 2 * wave + rg) + lr;
+  for (int j = 0; j < B8_DMA; j++) dma16_s(bb, st.boff[j], lds_addr(dst + 64 * (B8_DMA * wave + j)));
+}
+
+// fp16 weights (exact q) of 8 consecutive bytes, in the staged activations'
+// run order (0, 2, 1, 3, 4, 6, 5, 7).
+__device__ __forceinline__ h8_t q8_run(u2_t b) {
+  const uint32_t ex = 0x64646464u, a = b.x ^ 0x80808080u, c = b.y ^ 0x80808080u;
+  const h2_t m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  u4_t w;
+  w.x = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, a, 0x04020400u)) + m1152);
+  w.y = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, a, 0x04030401u)) + m1152);
+  w.z = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, c, 0x04020400u)) + m1152);
+  w.w = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, c, 0x04030401u)) + m1152);
+  return __builtin_bit_cast(h8_t, w);
+}
+
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void mfma_step_q8(TileStateQ8<GATEUP, NTT> &st, int kb) {
+  using S = TileStateQ8<GATEUP, NTT>;
+  constexpr int RG = S::RG, NMAT = S::NMAT, NKB = S::NKB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, g = lane >> 4;
+  wait_copies_and_barrier<VM_IN_FLIGHT>();
+  issue_b_q8(st, kb + 1 < NKB ? kb + 1 : NKB - 1);
+  issue_a(st, kb + A_AHEAD < NKB ? kb + A_AHEAD : NKB - 1);
+  const u4_t *as = &a_ring[kb % A_STAGES][0];
+  const u4_t *bt = &bt_st[kb & 1][0][0];
+  // LDS reads first: per row-block the four scales and this lane's 8 bytes of
+  // each block; per token tile the four activation fragments
+  f4_t dsc[RG][NMAT];
+  u2_t qb[RG][NMAT][4];
+#pragma unroll
+  for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+      const int rb = GATEUP ? m * RB_HALF + 16 * wave + lr : 16 * (2 * wave + rg) + lr;
+      dsc[rg][m] = __builtin_bit_cast(f4_t, as[rb * RB_CHUNKS]);
+      const u2_t *qp = reinterpret_cast<const u2_t *>(as + rb * RB_CHUNKS + 1);
+#pragma unroll
+      for (int b = 0; b < 4; b++) qb[rg][m][b] = qp[4 * b + g];
+    }
+  h8_t x[NTT][4];
+#pragma unroll
+  for (int t = 0; t < NTT; t++)
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+      x[t][b] = __builtin_bit_cast(h8_t, bt[16 * (16 * t + lr) + ((4 * b + g) ^ lr)]);
+  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    h8_t wf[RG][NMAT];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+      for (int m = 0; m < NMAT; m++) wf[rg][m] = q8_run(qb[rg][m][b]);
 #pragma unroll
     for (int t = 0; t < NTT; t++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int tok = 16 * t + 4 * g + i;
-        if (tok < n) {
-          const int slot = t_slot[tok];
-          if constexpr (GATEUP) {
-            h16m[(size_t)slot * F + perm8(r)] =
-                __float2half(silu(st.acc[rg][0][t][i]) * st.acc[rg][1][t][i]);
-          } else {
-            out[(size_t)slot * D + r] = st.acc[rg][0][t][i];
-          }
+      for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+          const f4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[t][b], wf[rg][m], zero4, 0, 0, 0);
+          const float d = dsc[rg][m][b];
+#pragma unroll
+          for (int i = 0; i < 4; i++) st.acc[rg][m][t][i] = __builtin_fmaf(d, p[i], st.acc[rg][m][t][i]);
         }
-      }
   }
+}
+
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void mfma_tile_q8(const uint8_t *__restrict__ wsh,
+                                             const __half *__restrict__ act, int n, int rt,
+                                             __half *__restrict__ h16m, float *__restrict__ out) {
+  using S = TileStateQ8<GATEUP, NTT>;
+  using C = MfmaCfg<GATEUP>;
+  constexpr int RG = S::RG, NMAT = S::NMAT, NKB = S::NKB, KD = C::KD;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  S st;
+  st.abase = wsh;
+#pragma unroll
+  for (int j = 0; j < A_DMA; j++) {
+    int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
+    if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
+    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
+    const int m = GATEUP ? rb / RB_HALF : 2, lrow = GATEUP ? rb % RB_HALF : rb;
+    st.aoff[j] = (uint32_t)(m * Q8_MAT_BYTES + (rt * C::TROWS + lrow) * NKB * QB + 16 * pc);
+  }
+  st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
+  // activations: copy j of wave w fills positions q = 64 (B8_DMA w + j) + lane
+  // of the 32 x 16 chunk tile: row r = q / 16, position q % 16 holds chunk
+  // (q % 16) ^ (r & 15). Rows past n copy token 0's row.
+  const int arow0 = t_arow[0];
+  st.bbase = reinterpret_cast<const uint8_t *>(act);
+#pragma unroll
+  for (int j = 0; j < B8_DMA; j++) {
+    const int q = 64 * (B8_DMA * wave + j) + lane, r = q >> 4;
+    const int ar = t_arow[r] >= 0 ? t_arow[r] : arow0;
+    st.boff[j] = (uint32_t)(2 * (ar * KD + 8 * ((q & 15) ^ (r & 15))));
+  }
+  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+      for (int t = 0; t < NTT; t++) st.acc[rg][m][t] = zero4;
+  issue_a(st, 0);
+  issue_b_q8(st, 0);
+#pragma unroll
+  for (int c = 1; c < A_AHEAD; c++) issue_a(st, c < NKB ? c : NKB - 1);
+  for (int kb = 0; kb < NKB; kb++) mfma_step_q8(st, kb);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  store_tile<GATEUP, NTT>(st.acc, n, rt, h16m, out);
 }
 
 // Launch order -> work item, so that consecutive work items run on one XCD
@@ -415,12 +571,14 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 // s, epilogue h = silu(g) * u -> h16m[slot][perm8(row)] (fp16). Otherwise
 // weights = down rows (K = 1536), activations = h16m, out[slot][row] fp32.
 // act_sum: sub-block sums of each activation row as (Sh, Sl, Sh, Sl) fp16.
+// wsh != nullptr: the shared expert's tiles use its Q8 matrices (mfma_tile_q8).
 template <bool GATEUP>
 __global__ __launch_bounds__(MT_THREADS) void k_moe_mfma(
-    const uint8_t *__restrict__ wq, const __half *__restrict__ act,
-    const __half *__restrict__ act_sum, const int32_t *__restrict__ list,
-    const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles, int T, int K,
-    __half *__restrict__ h16m, float *__restrict__ out) {
+    const uint8_t *__restrict__ wq, const uint8_t *__restrict__ wsh,
+    const __half *__restrict__ act, const __half *__restrict__ act_sum,
+    const int32_t *__restrict__ list, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ n_tiles, int T, int K, __half *__restrict__ h16m,
+    float *__restrict__ out) {
   using C = MfmaCfg<GATEUP>;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = w / C::NRT, rt = w % C::NRT;
@@ -435,10 +593,16 @@ __global__ __launch_bounds__(MT_THREADS) void k_moe_mfma(
     t_arow[tid] = s < 0 ? -1 : (GATEUP ? (s < T * K ? s / K : s - T * K) : s);
   }
   __syncthreads();
-  if (n > 16)
+  if (wsh && e == E) {
+    if (n > 16)
+      mfma_tile_q8<GATEUP, 2>(wsh, act, n, rt, h16m, out);
+    else
+      mfma_tile_q8<GATEUP, 1>(wsh, act, n, rt, h16m, out);
+  } else if (n > 16) {
     mfma_tile<GATEUP, 2>(wq, act, act_sum, e, n, rt, h16m, out);
-  else
+  } else {
     mfma_tile<GATEUP, 1>(wq, act, act_sum, e, n, rt, h16m, out);
+  }
 }
 
 // fp16 copy of s in the MFMA run order (perm8) for the gate/up activations,
@@ -460,11 +624,11 @@ __global__ __launch_bounds__(64) void k_hsums(const __half *__restrict__ h16m,
   row_subsums(h16m + (size_t)slot * F, F / 32, hsum + (size_t)slot * (F / 32) * 4);
 }
 
-template __global__ void k_moe_mfma<true>(const uint8_t *, const __half *, const __half *,
-                                          const int32_t *, const int4 *, const int32_t *, int,
-                                          int, __half *, float *);
-template __global__ void k_moe_mfma<false>(const uint8_t *, const __half *, const __half *,
-                                           const int32_t *, const int4 *, const int32_t *, int,
-                                           int, __half *, float *);
+template __global__ void k_moe_mfma<true>(const uint8_t *, const uint8_t *, const __half *,
+                                          const __half *, const int32_t *, const int4 *,
+                                          const int32_t *, int, int, __half *, float *);
+template __global__ void k_moe_mfma<false>(const uint8_t *, const uint8_t *, const __half *,
+                                           const __half *, const int32_t *, const int4 *,
+                                           const int32_t *, int, int, __half *, float *);
 
 }  // namespace hy3x

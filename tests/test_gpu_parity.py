@@ -395,3 +395,38 @@ def test_q4k_shared_restored_after_q8(torch, layer, cpu):
     y, ids, _, _ = run(torch, layer, x)
     yo, _ = cpu.forward(x)
     assert O.rel_l2(y - x, yo - x) <= TOL
+
+
+@pytest.mark.parametrize("T", [2, 40])
+def test_q8_shared_mfma_matches_oracle(torch, q8_layer, cpu, q8_mats, T):
+    """T >= 2 with hy3's Q8_0 shared expert: the MFMA grouped GEMM runs the
+    shared expert's tiles from its Q8 matrices (T = 40: one tile of 32 tokens
+    and one of 8)."""
+    x = O.normal(T * D, O.key(0xC1, 0, O.T_X), 1.0).reshape(T, D)
+    y, ids, wpre, w = run(torch, q8_layer, x)
+    yo, ro = q8_oracle(cpu, q8_mats, ids).forward(x)
+    assert np.array_equal(ids, ro["ids"])
+    assert O.rel_l2(y - x, yo - x) <= TOL
+    for t in range(T):
+        assert O.rel_l2(y[t] - x[t], yo[t] - x[t]) <= 2 * TOL, t
+
+
+def test_q8_shared_reference_tokens(torch, q8_layer):
+    """hy3.c's forward_layer_moe with the Q8_0 shared expert on three config-1
+    tokens (moe_q8.npz), through the batched (MFMA) path."""
+    f = np.load(os.path.join(G, "moe_q8.npz"))
+    y_ref = f["c1/y"]
+    x = O.normal(y_ref.size, O.key(0xC1, 0, O.T_X), 1.0).reshape(y_ref.shape)
+    y = run(torch, q8_layer, x)[0]
+    assert O.rel_l2(y - x, y_ref - x) <= TOL
+
+
+def test_q8_shared_gemv_path_is_refused(torch, q8_layer):
+    """The GEMV tile path has no Q8 kernels: forcing it fails loudly."""
+    x = O.normal(2 * D, O.key(0xC1, 0, O.T_X), 1.0).reshape(2, D)
+    q8_layer.set_path(1)
+    try:
+        with pytest.raises(H.HY3XError):
+            run(torch, q8_layer, x)
+    finally:
+        q8_layer.set_path(0)
