@@ -49,6 +49,9 @@ def parse():
     p.add_argument("--shared-q8", action="store_true",
                    help="shared expert in hy3's Q8_0, the type real checkpoints carry "
                         "(the configs' default is Q4_K)")
+    p.add_argument("--residual", action="store_true",
+                   help="time hy3x_layer_forward_residual (x += attn_out fused in front of "
+                        "the block, as add_rmsnorm_kernel + gpu_ffn_moe)")
     p.add_argument("--graph", action="store_true",
                    help="replay a HIP graph of each step's kernels instead of launching them "
                         "directly (measured slower than direct launches on ROCm 7.2)")
@@ -124,7 +127,8 @@ def dominant_kernel(stage, T, path):
     return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
 
 
-def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=False):
+def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=False,
+            residual=False):
     layers = []
     for li in range(cfg.n_layers):
         L = H.MoELayer(cfg.T)
@@ -137,11 +141,16 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
             L.set_path(path)
         layers.append(L)
     x = torch.from_numpy(C.inputs(cfg.input_seed, cfg.T).copy()).cuda()
+    # residual addend (attention output stand-in): a small multiple of other inputs
+    attn = torch.from_numpy(C.inputs(cfg.input_seed + 1, cfg.T).copy() * 0.01).cuda()
     stream = torch.cuda.current_stream().cuda_stream
 
     def eager_step():
         for L in layers:
-            L.forward(x.data_ptr(), cfg.T, cfg.K, stream=stream)
+            if residual:
+                L.forward_residual(x.data_ptr(), attn.data_ptr(), cfg.T, cfg.K, stream=stream)
+            else:
+                L.forward(x.data_ptr(), cfg.T, cfg.K, stream=stream)
 
     step = eager_step
     if use_graph:
@@ -263,7 +272,7 @@ def main():
     cfg = C.CONFIGS[a.config]
     steps = a.steps or default_steps(cfg.T, cfg.n_layers)
     r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph, path=a.path,
-                shared_q8=a.shared_q8)
+                shared_q8=a.shared_q8, residual=a.residual)
     out = {
         "metric": "MoE-layer tokens/s (decode B=1) and achieved HBM GB/s vs peak",
         "value": round(r["tokens_per_s"], 2),
@@ -278,7 +287,8 @@ def main():
                    "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu",
                    "launch": "hip-graph" if a.graph else "direct",
                    "expert_path": ["auto", "gemv", "mfma"][a.path],
-                   "shared_expert": "q8_0" if a.shared_q8 else "q4_k"},
+                   "shared_expert": "q8_0" if a.shared_q8 else "q4_k",
+                   "entry": "forward_residual" if a.residual else "forward"},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),
                   "hbm_frac": round(r["layer_GBps"] / PEAK_HBM_GBS, 4),
                   "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},

@@ -55,6 +55,7 @@ _SIGS = {
     "hy3x_synth_shared_q8_0": (I32, [P, U64, U32]),
     "hy3x_synth_quantize_q8_0": (I32, [P, P, I64, P]),
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
+    "hy3x_layer_forward_residual": (I32, [P, P, P, I32, I32, F32, P]),
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
     "hy3x_layer_time_stage": (I32, [P, I32, I32, P, ctypes.POINTER(ctypes.c_float)]),
@@ -218,6 +219,12 @@ class MoELayer:
     def forward(self, x_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE, stream=None):
         """In-place MoE block on device memory x[T x 4096] (fp32)."""
         _check(lib().hy3x_layer_forward(self._h, x_dev_ptr, T, K, scale, stream))
+
+    def forward_residual(self, x_dev_ptr, attn_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE,
+                         stream=None):
+        """x += attn_out, then the MoE block, in one forward (hy3x_layer_forward_residual)."""
+        _check(lib().hy3x_layer_forward_residual(self._h, x_dev_ptr, attn_dev_ptr, T, K, scale,
+                                                 stream))
 
     def last_routing(self, T, K):
         ids = np.empty((T, K), np.int32)

@@ -268,7 +268,8 @@ __device__ __forceinline__ void down_passes(const uint8_t *wl, const uint32_t (&
 __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
     const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
-    float *__restrict__ x, const uint8_t *__restrict__ wsh, unsigned long long *trace) {
+    float *__restrict__ x, const float *__restrict__ xadd, const uint8_t *__restrict__ wsh,
+    unsigned long long *trace) {
   constexpr int RPB = DEC_DOWN_RPB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[KMAX + 1][DN_WAVE_B];
   __shared__ float out_l[KMAX + 1][RPB];
@@ -311,7 +312,8 @@ __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
     const int r = r0 + threadIdx.x;
     float eo = 0.0f;
     for (int kk = 0; kk < K; kk++) eo = __builtin_fmaf(w[kk], out_l[kk][threadIdx.x], eo);
-    x[r] = x[r] + (out_l[K][threadIdx.x] + eo);
+    const float xr = xadd ? x[r] + xadd[r] : x[r];
+    x[r] = xr + (out_l[K][threadIdx.x] + eo);
   }
   trace_point(trace, 3);
 }
@@ -320,6 +322,7 @@ __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
 // 1318-1319, 1324-1325). Block (c, t): elements 1024 c .. 1024 c + 1023 of
 // token t, four per thread; every slot's row is loaded before the FMA chain.
 __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
+                                                 const float *__restrict__ xadd,
                                                  const float *__restrict__ out,
                                                  const float *__restrict__ w, int T, int K) {
   const int t = blockIdx.y, i = blockIdx.x * 1024 + 4 * threadIdx.x;
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
       wk[k] = w[t * K + k];
     }
   const float4 sh = *reinterpret_cast<const float4 *>(out + (size_t)(T * K + t) * D + i);
-  float4 xv = *reinterpret_cast<const float4 *>(x + (size_t)t * D + i);
+  float4 xv = load_x4(x + (size_t)t * D, xadd ? xadd + (size_t)t * D : nullptr, i / 4);
   float4 eo = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int k = 0; k < KMAX; k++)

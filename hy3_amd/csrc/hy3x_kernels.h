@@ -4,11 +4,13 @@
 
 namespace hy3x {
 
-__global__ void k_router_logits(const float *x, const float *norm_w, const float *router,
+__global__ void k_router_logits(const float *x, const float *xadd, const float *norm_w,
+                                const float *router,
                                 const float *bias, int has_bias, float *logits, float *sig,
                                 float *score, __half *s16, float *s32,
                                 unsigned long long *trace, int T, uint32_t *bits, int wt);
-__global__ void k_rmsnorm(const float *x, const float *norm_w, __half *s16, float *s32,
+__global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w, __half *s16,
+                          float *s32,
                           __half *s16m, __half *ssum, int T, uint32_t *bits, int wt);
 template <int MT, int ME, int TG, int EG>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
@@ -36,17 +38,20 @@ __global__ void k_gateup_decode(const uint8_t *wq, const __half *s16, const floa
                                 const float *score, int K, float scale, int32_t *ids,
                                 float *wpre, float *wout, unsigned long long *stats,
                                 __half *h16, unsigned long long *trace);
-__global__ void k_route_decode(const float *x, const float *norm_w, const float *router,
+__global__ void k_route_decode(const float *x, const float *xadd, const float *norm_w,
+                               const float *router,
                                const float *bias, int has_bias, int K, float *logits,
                                float *sig, float *score, __half *s16, float *s32,
                                const uint8_t *wq, const uint8_t *wsh, __half *h16,
                                unsigned long long *trace);
 __global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *ids,
-                              const float *w, int K, float *x, const uint8_t *wsh,
+                              const float *w, int K, float *x, const float *xadd,
+                              const uint8_t *wsh,
                               unsigned long long *trace);
 __global__ void k_repack_q8x128(const uint8_t *src, uint8_t *dst, int64_t n_super);
 __global__ void k_synth_q8_0(uint8_t *dst, int64_t nblocks, uint64_t key, const float *src);
-__global__ void k_combine(float *x, const float *out, const float *w, int T, int K);
+__global__ void k_combine(float *x, const float *xadd, const float *out, const float *w, int T,
+                          int K);
 
 extern template __global__ void k_gateup_gemv<1>(const uint8_t *, const __half *, const int32_t *,
                                                  const int4 *, const int32_t *, int, int,

@@ -47,6 +47,7 @@ struct hy3x_layer {
   int last_T = 0, last_K = 0;
   struct Forward {  // launch parameters of the current / last forward
     float *x = nullptr;
+    const float *xadd = nullptr;  // residual addend (hy3x_layer_forward_residual) or null
     int T = 0, K = 0, nt = 4, mt = 0;
     float scale = 1.0f;
     Mode mode = Mode::GEMV;
@@ -285,20 +286,20 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
     case HY3X_STAGE_ROUTER:
       if (c.mode == Mode::DECODE) {
         k_route_decode<<<E + DEC_GU_BLOCKS, 256, 0, st>>>(
-            x, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
+            x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
             L->s16, L->s32, L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16, L->trace[0]);
         break;
       }
       // the routing kernels also clear (first kernel) and fill (top-K) the
       // dispatch bitmaps; for T > 8 the RMSNorm kernel stages the MFMA operand
       if (T <= kSmallRouterT) {
-        k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, L->norm_w, L->router, L->bias,
+        k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, c.xadd, L->norm_w, L->router, L->bias,
                                                     L->has_bias, L->logits, L->sig, L->score,
                                                     L->s16, L->s32, L->trace[0], T, L->bits,
                                                     L->wt);
       } else {
         const bool mf = c.mode == Mode::MFMA;
-        k_rmsnorm<<<T, 256, 0, st>>>(x, L->norm_w, mf ? nullptr : L->s16, L->s32,
+        k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : L->s16, L->s32,
                                      mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt);
         if (T <= kMidRouterT)
           k_router_gemm<2, 2, 4, 8><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
@@ -338,7 +339,8 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
         k_down_decode<<<D / DEC_DOWN_RPB, 64 * (KMAX + 1), 0, st>>>(
-            L->wq, L->h16, L->ids, L->w, K, x, L->shared_q8 ? L->wsh : nullptr, L->trace[2]);
+            L->wq, L->h16, L->ids, L->w, K, x, c.xadd, L->shared_q8 ? L->wsh : nullptr,
+            L->trace[2]);
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
         k_moe_mfma<false><<<mt * (D / (32 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16m, L->hsum, L->list,
@@ -350,12 +352,27 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                       L->n_tiles, L->out);
       break;
     case HY3X_STAGE_COMBINE:
-      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 1024, T), 256, 0, st>>>(x, L->out, L->w, T, K);
+      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 1024, T), 256, 0, st>>>(x, c.xadd, L->out, L->w, T, K);
       break;
   }
 }
 
+static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K, float scale,
+                        void *stream);
+
 int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
+  return forward_impl(L, x, nullptr, T, K, scale, stream);
+}
+
+int hy3x_layer_forward_residual(hy3x_layer *L, float *x, const float *attn_out, int T, int K,
+                                float scale, void *stream) {
+  if (!attn_out) return fail(HY3X_E_ARG, "NULL attn_out");
+  if (attn_out == x) return fail(HY3X_E_ARG, "attn_out must not alias x");
+  return forward_impl(L, x, attn_out, T, K, scale, stream);
+}
+
+static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K, float scale,
+                        void *stream) {
   if (!L || !x) return fail(HY3X_E_ARG, "NULL argument");
   if (T < 1 || T > L->max_tokens) return fail(HY3X_E_ARG, "T=%d outside [1,%d]", T, L->max_tokens);
   if (K < 1 || K > KMAX) return fail(HY3X_E_ARG, "K=%d outside [1,8]", K);
@@ -363,6 +380,7 @@ int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void 
   hipStream_t st = (hipStream_t)stream;
   auto &c = L->cur;
   c.x = x;
+  c.xadd = xadd;
   c.T = T;
   c.K = K;
   c.scale = scale;

@@ -71,22 +71,23 @@ __device__ __forceinline__ float chain_dot(const float *a, const float *b) {
 // sum of squares in the fixed block order, then lanes 0..7 run the eight
 // logit chains. Block (0, t) also stages s for the expert kernels.
 __device__ __forceinline__ void router_block(
-    int e, int t, const float *__restrict__ x, const float *__restrict__ norm_w,
-    const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
-    float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
-    __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace) {
+    int e, int t, const float *__restrict__ x, const float *__restrict__ xadd,
+    const float *__restrict__ norm_w, const float *__restrict__ router,
+    const float *__restrict__ bias, int has_bias, float *__restrict__ logits,
+    float *__restrict__ sig, float *__restrict__ score, __half *__restrict__ s16,
+    float *__restrict__ s32, unsigned long long *trace) {
   __shared__ __attribute__((aligned(16))) float xsf[8 * RS], wsf[8 * RS], rsf[8 * RS];
   const int tid = threadIdx.x;
   trace_point(trace, 0);
   float r_blk;
   {  // every load in flight at once: 4 float4 of each row per thread
-    const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)t * D);
+    const float *xt = x + (size_t)t * D, *at = xadd ? xadd + (size_t)t * D : nullptr;
     const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
     const float4 *rg = reinterpret_cast<const float4 *>(router + (size_t)e * D);
     float4 a[4], b[4], c[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      a[u] = xg[tid + 256 * u];
+      a[u] = load_x4(xt, at, tid + 256 * u);
       b[u] = wg[tid + 256 * u];
       c[u] = rg[tid + 256 * u];
     }
@@ -127,14 +128,14 @@ __device__ __forceinline__ void router_block(
 }
 
 __global__ __launch_bounds__(256) void k_router_logits(
-    const float *__restrict__ x, const float *__restrict__ norm_w,
+    const float *__restrict__ x, const float *__restrict__ xadd, const float *__restrict__ norm_w,
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
     __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace, int T,
     uint32_t *__restrict__ bits, int wt) {
   if (bits) dispatch_clear_part(T, bits, wt, blockIdx.y * E + blockIdx.x, E * T);
-  router_block(blockIdx.x, blockIdx.y, x, norm_w, router, bias, has_bias, logits, sig, score, s16,
-               s32, trace);
+  router_block(blockIdx.x, blockIdx.y, x, xadd, norm_w, router, bias, has_bias, logits, sig,
+               score, s16, s32, trace);
 }
 
 // Single token: router logits and the shared expert's gate/up in one launch.
@@ -146,26 +147,25 @@ __global__ __launch_bounds__(256) void k_router_logits(
 // (k_gateup_decode): publishing it from here would need a device-scope
 // release/acquire between blocks, which costs more than recomputing it.
 __global__ __launch_bounds__(256) void k_route_decode(
-    const float *__restrict__ x, const float *__restrict__ norm_w,
+    const float *__restrict__ x, const float *__restrict__ xadd, const float *__restrict__ norm_w,
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias, int K,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
     __half *__restrict__ s16, float *__restrict__ s32, const uint8_t *__restrict__ wq,
     const uint8_t *__restrict__ wsh, __half *__restrict__ h16, unsigned long long *trace) {
   const int tid = threadIdx.x;
   if (blockIdx.x < E) {
-    router_block(blockIdx.x, 0, x, norm_w, router, bias, has_bias, logits, sig, score, s16, s32,
-                 trace);
+    router_block(blockIdx.x, 0, x, xadd, norm_w, router, bias, has_bias, logits, sig, score, s16,
+                 s32, trace);
     return;
   }
   // shared expert: s = rmsnorm(x) * norm_w, pair-staged fp16 in LDS
   trace_point(trace, 0);
   __shared__ __attribute__((aligned(16))) __half s_l[D];
   __shared__ float red_l[4];
-  const float4 *xg = reinterpret_cast<const float4 *>(x);
   const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
   float4 a[4];
 #pragma unroll
-  for (int u = 0; u < 4; u++) a[u] = xg[tid + 256 * u];
+  for (int u = 0; u < 4; u++) a[u] = load_x4(x, xadd, tid + 256 * u);
   const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
 #pragma unroll
   for (int u = 0; u < 4; u++) {
@@ -195,6 +195,7 @@ __global__ __launch_bounds__(256) void k_route_decode(
 // (2) router GEMM, LDS-tiled SIMT, each output keeping its eight chains;
 // (3) top-K, one wave per token.
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
+                                                 const float *__restrict__ xadd,
                                                  const float *__restrict__ norm_w,
                                                  __half *__restrict__ s16,
                                                  float *__restrict__ s32,
@@ -203,11 +204,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
                                                  uint32_t *__restrict__ bits, int wt) {
   const int t = blockIdx.x, tid = threadIdx.x;
   if (bits) dispatch_clear_part(T, bits, wt, t, T);
-  const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)t * D);
+  const float *xt = x + (size_t)t * D, *at = xadd ? xadd + (size_t)t * D : nullptr;
   const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
   float4 a[4];
 #pragma unroll
-  for (int u = 0; u < 4; u++) a[u] = xg[tid + 256 * u];
+  for (int u = 0; u < 4; u++) a[u] = load_x4(xt, at, tid + 256 * u);
   __shared__ float red_l[4];
   const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
 #pragma unroll

@@ -110,6 +110,18 @@ int hy3x_layer_expert_ptr(hy3x_layer *layer, int expert, int matrix, void **ptr)
  * the reference's ctx singleton buffers (hy3_gpu.cu:483, 616-621). */
 int hy3x_layer_forward(hy3x_layer *layer, float *x, int T, int K, float scale, void *stream);
 
+/* The residual add before the block fused into it: x += attn_out, then the
+ * MoE block on the new x, i.e. hy3.c:1264-1266 (x[i] += s2[i]; rms_norm...)
+ * and the GPU engine's add_rmsnorm_kernel + gpu_ffn_moe (hy3_gpu.cu:453-460,
+ * 761-762), without the separate add kernel and its 16 KB-per-token round
+ * trip: every kernel that reads x forms x + attn_out itself (the same fp32
+ * add), and the final write is (x + attn_out) + (shared + sum_k w_k expert_k).
+ * attn_out: device [T x 4096] fp32, read only, must not alias x. Otherwise
+ * as hy3x_layer_forward (its result equals forward on x + attn_out bit for
+ * bit). */
+int hy3x_layer_forward_residual(hy3x_layer *layer, float *x, const float *attn_out, int T, int K,
+                                float scale, void *stream);
+
 /* Routing of the last forward, copied to host buffers (synchronises on the
  * stream): ids[T x K] int32 in selection order, wpre[T x K] = sigma / sum
  * (before the scale), w[T x K] (after). Any pointer may be NULL. */

@@ -430,3 +430,31 @@ def test_q8_shared_gemv_path_is_refused(torch, q8_layer):
             run(torch, q8_layer, x)
     finally:
         q8_layer.set_path(0)
+
+
+@pytest.mark.parametrize("T", [1, 40, 300])
+def test_forward_residual_equals_add_then_forward(torch, layer, cpu, T):
+    """hy3x_layer_forward_residual(x, a) == hy3x_layer_forward(x + a) bit for bit
+    (every reader forms the same fp32 x + a), a is left unchanged, and the
+    result matches the oracle on x + a."""
+    set_bias(layer, cpu, "uniform")
+    x = O.normal(T * D, O.key(0xC1, 0, O.T_X), 1.0).reshape(T, D)
+    a = (O.normal(T * D, O.key(0xC2, 0, O.T_X), 1.0) * np.float32(0.5)).reshape(T, D)
+    xd = torch.from_numpy(x.copy()).cuda()
+    ad = torch.from_numpy(a.copy()).cuda()
+    layer.forward_residual(xd.data_ptr(), ad.data_ptr(), T)
+    torch.cuda.synchronize()
+    y1 = xd.cpu().numpy()
+    assert np.array_equal(ad.cpu().numpy(), a)
+    xa = (x + a).astype(np.float32)
+    y2 = run(torch, layer, xa)[0]
+    assert np.array_equal(y1, y2)
+    if T == 1:
+        yo, _ = cpu.forward(xa)
+        assert O.rel_l2(y1 - xa, yo - xa) <= TOL
+
+
+def test_forward_residual_rejects_alias(torch, layer):
+    xd = torch.zeros(D, dtype=torch.float32, device="cuda")
+    with pytest.raises(H.HY3XError):
+        layer.forward_residual(xd.data_ptr(), xd.data_ptr(), 1)
