@@ -52,6 +52,8 @@ _SIGS = {
     "hy3x_layer_set_expert_q4k": (I32, [P, I32, P, P, P, I32]),
     "hy3x_layer_expert_ptr": (I32, [P, I32, I32, ctypes.POINTER(P)]),
     "hy3x_layer_set_shared_q8_0": (I32, [P, P, P, P, I32]),
+    "hy3x_layer_load_gguf": (I32, [P, ctypes.c_char_p, I32]),
+    "hy3x_gguf_check_layer": (I32, [ctypes.c_char_p, I32, ctypes.POINTER(I32)]),
     "hy3x_synth_shared_q8_0": (I32, [P, U64, U32]),
     "hy3x_synth_quantize_q8_0": (I32, [P, P, I64, P]),
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
@@ -129,6 +131,14 @@ def synth_zipf_bias(n_expert, seed):
     return out
 
 
+def gguf_check_layer(path, layer_index):
+    """Validate a hy3 GGUF file's MoE tensors for one layer (no GPU needed);
+    returns the shared expert's ggml type (8: hy3 Q8_0, 12: Q4_K)."""
+    t = I32()
+    _check(lib().hy3x_gguf_check_layer(os.fsencode(path), layer_index, ctypes.byref(t)))
+    return t.value
+
+
 class MoELayer:
     """One Hy3 MoE FFN layer resident on the current HIP device."""
 
@@ -180,6 +190,10 @@ class MoELayer:
             assert gate.size == up.size == down.size == Q8_0_MATRIX_BYTES
         _check(lib().hy3x_layer_set_shared_q8_0(self._h, _ptr(gate), _ptr(up), _ptr(down),
                                                 1 if on_device else 0))
+
+    def load_gguf(self, path, layer_index):
+        """Router, norm, bias and all 193 experts of one layer from a hy3 GGUF file."""
+        _check(lib().hy3x_layer_load_gguf(self._h, os.fsencode(path), layer_index))
 
     def synth_shared_q8_0(self, seed, layer_index=0):
         _check(lib().hy3x_synth_shared_q8_0(self._h, seed, layer_index))

@@ -88,6 +88,11 @@ static int fail(int code, const char *fmt, ...) {
   return code;
 }
 
+// The error channel for the library's other translation units (GGUF loader).
+namespace hy3x {
+int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
+}  // namespace hy3x
+
 #define HIP_TRY(call)                                                                  \
   do {                                                                                 \
     hipError_t e_ = (call);                                                            \

@@ -97,6 +97,24 @@ int hy3x_layer_set_expert_q4k(hy3x_layer *layer, int expert, const void *gate, c
 int hy3x_layer_set_shared_q8_0(hy3x_layer *layer, const void *gate, const void *up,
                                const void *down, int src_on_device);
 
+/* The MoE tensors of layer `layer_index` straight from a hy3 GGUF file (the
+ * converter's names, hy3_convert.c:960-1035, bound as hy3.c:740-787 binds
+ * them): blk.N.ffn_norm.weight (F32), blk.N.ffn_gate_inp.weight (F32
+ * [192 x 4096]), blk.N.ffn_gate_exps_b.bias (F32 [192], optional: no bias
+ * when absent, hy3.c:781-787), blk.N.ffn_{gate,up,down}_exps.E.{gate,up,
+ * down}_proj.weight (Q4_K) for E in 0..191, and blk.N.ffn_{gate,up,
+ * down}_shexp.weight (hy3 Q8_0, or Q4_K). The file is memory-mapped
+ * read-only and parsed with bounds checks (GGUF v2/v3, general.alignment);
+ * every tensor's type and shape is checked before anything is uploaded.
+ * Replaces the MoE part of hy3_model_load's binding and of hy3_gpu_init's
+ * upload (hy3.c:740-787; hy3_gpu.cu:580-595). Errors: HY3X_E_ARG with the
+ * offending tensor named in hy3x_last_error(). */
+int hy3x_layer_load_gguf(hy3x_layer *layer, const char *path, int layer_index);
+/* The same checks without a layer or a GPU: 0 if the file holds every MoE
+ * tensor of layer `layer_index` with the expected type and shape;
+ * *shared_type (may be NULL) receives the shared expert's ggml type (8 or 12). */
+int hy3x_gguf_check_layer(const char *path, int layer_index, int *shared_type);
+
 /* Device address of expert e's matrix m (0 gate, 1 up, 2 down) inside the
  * layer's weight arena, for callers that fill the arena directly. */
 int hy3x_layer_expert_ptr(hy3x_layer *layer, int expert, int matrix, void **ptr);

@@ -21,8 +21,12 @@ Runs ONLY in a container that holds the reference sources at /root/reference
                     and the Q8_0 bytes read back from the GGUF it writes
   moe_q8.npz        forward_layer_moe with the shared expert in hy3's Q8_0 (the type real
                     checkpoints carry), on config-0/1 tokens
+  convert_small.gguf  the converter's output for a small safetensors directory holding one
+                    MoE layer's tensor kinds (norm, router, bias, a routed expert, a shared
+                    expert) at small shapes: the GGUF framing the writer and the library's
+                    loader are checked against
 
-Usage: python tests/golden/make_fixtures.py [--only q8]   (all: about 2 minutes on 8 cores)
+Usage: python tests/golden/make_fixtures.py [--only q8|gguf]   (all: about 2 minutes on 8 cores)
 """
 import argparse
 import hashlib
@@ -110,9 +114,25 @@ def q8_fixtures(R, lay_seed=0xC0):
     np.savez_compressed(os.path.join(OUT, "moe_q8.npz"), **fx)
 
 
+def gguf_fixture(R):
+    rng = np.random.default_rng(9)
+    t = {
+        "model.layers.1.post_attention_layernorm.weight": rng.standard_normal(256),
+        "model.layers.1.mlp.router.gate.weight": rng.standard_normal((4, 256)) * 0.02,
+        "model.layers.1.mlp.expert_bias": rng.uniform(-0.1, 0.1, 4),
+        "model.layers.1.mlp.experts.3.gate_proj.weight": rng.standard_normal((2, 256)) * 0.02,
+        "model.layers.1.mlp.shared_mlp.down_proj.weight": rng.standard_normal((2, 64)) * 0.02,
+    }
+    with tempfile.TemporaryDirectory() as d:
+        write_safetensors_dir(d, {k: np.asarray(v, np.float32) for k, v in t.items()})
+        out = os.path.join(OUT, "convert_small.gguf")
+        assert R.hy3ref_convert(d.encode(), out.encode(), 12) == 0
+    print("gguf fixture written", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", choices=["q8"], default=None)
+    ap.add_argument("--only", choices=["q8", "gguf"], default=None)
     a = ap.parse_args()
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref", f"REF={REF}"],
                    check=True)
@@ -120,6 +140,9 @@ def main():
     assert R is not None
     if a.only == "q8":
         q8_fixtures(R)
+        return
+    if a.only == "gguf":
+        gguf_fixture(R)
         return
     meta = {
         "reference": REF,
@@ -284,6 +307,7 @@ def main():
     lay.bias = uni_bias
     np.savez_compressed(os.path.join(OUT, "moe.npz"), **fx)
     q8_fixtures(R)
+    gguf_fixture(R)
     print("all fixtures written", flush=True)
 
 

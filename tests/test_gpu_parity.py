@@ -458,3 +458,41 @@ def test_forward_residual_rejects_alias(torch, layer):
     xd = torch.zeros(D, dtype=torch.float32, device="cuda")
     with pytest.raises(H.HY3XError):
         layer.forward_residual(xd.data_ptr(), xd.data_ptr(), 1)
+
+
+def test_load_gguf_layer_matches_source(torch, q8_layer, cpu, q8_mats, tmp_path):
+    """A whole layer written as a hy3 GGUF file (the converter's framing, tensor
+    names and types: Q4_K routed experts, Q8_0 shared expert, F32 router, norm
+    and bias) and loaded by hy3x_layer_load_gguf computes exactly what the
+    layer it came from computes (T = 1 and T = 40)."""
+    import sys
+    sys.path.insert(0, G)
+    from gguf_write import write_gguf
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    il = 7
+    t = [(f"blk.{il}.ffn_norm.weight", 0, [D], nw.view(np.uint8)),
+         (f"blk.{il}.ffn_gate_inp.weight", 0, [E, D], rt.view(np.uint8)),
+         (f"blk.{il}.ffn_gate_exps_b.bias", 0, [E], b.view(np.uint8))]
+    kinds = ("gate", "up", "down")
+    for e in range(E):
+        for m, kind in enumerate(kinds):
+            dims = [D, 1536] if kind == "down" else [1536, D]
+            t.append((f"blk.{il}.ffn_{kind}_exps.{e}.{kind}_proj.weight", 12, dims,
+                      cpu.expert(e)[m]))
+    for m, kind in enumerate(kinds):
+        dims = [D, 1536] if kind == "down" else [1536, D]
+        t.append((f"blk.{il}.ffn_{kind}_shexp.weight", 8, dims, q8_mats[m]))
+    path = tmp_path / "layer.gguf"
+    write_gguf(path, t)
+    assert H.gguf_check_layer(path, il) == 8
+    L2 = H.MoELayer(64)
+    try:
+        L2.load_gguf(path, il)
+        for T in (1, 40):
+            x = O.normal(T * D, O.key(0xC2, 0, O.T_X), 1.0).reshape(T, D)
+            y1 = run(torch, q8_layer, x)[0]
+            y2 = run(torch, L2, x)[0]
+            assert np.array_equal(y1, y2), T
+    finally:
+        L2.close()
+        path.unlink()
