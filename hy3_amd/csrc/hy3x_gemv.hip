@@ -11,7 +11,6 @@
 #include "hy3x_q4k.h"
 #include "hy3x_decode.h"
 #include "hy3x_route.h"
-#include "hy3x_dma.h"
 #include "hy3x_q8.h"
 
 namespace hy3x {
@@ -205,107 +204,37 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
   trace_point(trace, 3);
 }
 
-// Down of a single token for rows blockIdx.x*16 .. +16, fused with the
+// Down of a single token for rows blockIdx.x*RPB .. +RPB, fused with the
 // combine y = x + (shared + sum_k w_k * down_k), k in selection order
 // (hy3.c:1302, 1318-1319, 1324-1325). Wave k owns slot k (k < K routed,
-// k = K the shared expert). Its 16 rows of the expert's down matrix are one
-// contiguous 13,824-byte range; the wave copies that range and its 3,072-byte
-// h slot straight into LDS with every copy issued at once (2.25 waves per
-// SIMD cannot keep enough bytes in flight from registers), then computes
-// each pass of 2 rows as soon as the copies holding them have landed. The
-// row sums go to LDS and 16 threads combine them. wsh != nullptr: the shared
-// expert is the layer's Q8 one (hy3x_q8.h); its wave streams its rows (twice
-// the bytes, more than its LDS share holds) through registers instead.
-namespace {
-constexpr int DN_ROWB = (F / QK) * QB;                          // 864 B per down row
-constexpr int DN_WB = DEC_DOWN_RPB * DN_ROWB;                   // 13,824 B per wave
-constexpr int DN_NW = (DN_WB + 1023) / 1024;                    // 14 weight copies
-constexpr int DN_LAST_LANES = (DN_WB - 1024 * (DN_NW - 1)) / 16;  // 32 lanes in the last
-constexpr int DN_NH = F * 2 / 1024;                             // 3 copies of h
-constexpr int DN_WAVE_B = 1024 * (DN_NH + DN_NW);               // 17,408 B of LDS per wave
-static_assert(DEC_DOWN_RPB == 16, "k_down_decode: 16 rows per block");
-static_assert(DN_WB % 16 == 0 && F * 2 == 1024 * DN_NH, "copy granularity");
-
-// copies pending once pass ps (rows 2ps, 2ps+1) is in: all weight copies past
-// the last one that holds bytes of row 2ps+1
-constexpr int dn_pending(int ps) {
-  return DN_NW - (2 * DN_ROWB * (ps + 1) + 1023) / 1024;
-}
-
-template <int PS>
-__device__ __forceinline__ void down_pass(const uint8_t *wl, const uint32_t (&X)[32], float slo,
-                                          float shi, int gl, int hw, const ScaleSel &sel,
-                                          float *out_k) {
-  wait_vm<dn_pending(PS)>();
-  const uint8_t *row = wl + (2 * PS + hw) * DN_ROWB + (gl >> 2) * QB;
-  const uint4 hdr = *reinterpret_cast<const uint4 *>(row);
-  const uint4 q0 = *reinterpret_cast<const uint4 *>(row + 16 + 32 * (gl & 3));
-  const uint4 q1 = *reinterpret_cast<const uint4 *>(row + 32 + 32 * (gl & 3));
-  float dv = 0.0f;
-  if (gl < F / 64) {
-    uint32_t P[32];
-    unpack_group(q0, q1, P);
-    dv = group_dot(P, X, slo, shi, block_scale(hdr, sel));
-  }
-  const float2 t = half_totals(dv);
-  if ((threadIdx.x & 63) == 0) {
-    out_k[2 * PS] = t.x;
-    out_k[2 * PS + 1] = t.y;
-  }
-}
-
-template <int PS>
-__device__ __forceinline__ void down_passes(const uint8_t *wl, const uint32_t (&X)[32], float slo,
-                                            float shi, int gl, int hw, const ScaleSel &sel,
-                                            float *out_k) {
-  if constexpr (PS < DEC_DOWN_RPB / 2) {
-    down_pass<PS>(wl, X, slo, shi, gl, hw, sel, out_k);
-    down_passes<PS + 1>(wl, X, slo, shi, gl, hw, sel, out_k);
-  }
-}
-}  // namespace
-
+// k = K the shared expert): its passes of 2 rows stream through a register
+// ring of DEC_DOWN_PF passes (down_rows; 2 measured best), the row sums go
+// to LDS, and DEC_DOWN_RPB threads combine them. wsh != nullptr: the shared
+// expert is the layer's Q8 one (down_rows_q8). A variant that copied each
+// wave's 16 rows into LDS with every copy in flight at once measured faster
+// in back-to-back replays of this kernel alone but slower inside the
+// forward (decode 32.9 vs 32.1 us, 79-layer stack 2.87 vs 2.82 ms): its
+// 157 KB of LDS per block keeps a block off a CU until the CU is empty.
 __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
     const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
     float *__restrict__ x, const float *__restrict__ xadd, const uint8_t *__restrict__ wsh,
     unsigned long long *trace) {
   constexpr int RPB = DEC_DOWN_RPB;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[KMAX + 1][DN_WAVE_B];
   __shared__ float out_l[KMAX + 1][RPB];
   trace_point(trace, 0);
-  const int lane = threadIdx.x & 63;
-  const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int r0 = blockIdx.x * RPB;
-  if (k == K && wsh) {
-    down_rows_q8<RPB / 2, 2>(wsh, h16 + (size_t)K * F, r0, [&](int ps, float2 t) {
-      if (lane == 0) {
-        out_l[K][2 * ps] = t.x;
-        out_l[K][2 * ps + 1] = t.y;
-      }
-    });
-  } else if (k <= K) {
-    const int e = k < K ? __builtin_amdgcn_readfirstlane(ids[k]) : E;
-    uint8_t *hl = lds[k], *wl = lds[k] + 1024 * DN_NH;
-    const uint8_t *hsrc = reinterpret_cast<const uint8_t *>(h16 + (size_t)k * F) + 16 * lane;
-#pragma unroll
-    for (int j = 0; j < DN_NH; j++) dma16(hsrc + 1024 * j, lds_addr(hl + 1024 * j));
-    const uint8_t *src = wq + (size_t)e * EXPERT_BYTES + 2 * MAT_BYTES + (size_t)r0 * DN_ROWB +
-                         16 * lane;
-#pragma unroll
-    for (int j = 0; j < DN_NW; j++)
-      if (j < DN_NW - 1 || lane < DN_LAST_LANES) dma16(src + 1024 * j, lds_addr(wl + 1024 * j));
-    wait_vm<DN_NW>();  // h is in
-    const int hw = lane >> 5, gl = lane & 31;
-    uint32_t X[32];
-    float slo = 0.0f, shi = 0.0f;
-    if (gl < F / 64) {
-      load_group_x(reinterpret_cast<const __half *>(hl), gl, X);
-      group_sums(X, slo, shi);
+  auto keep = [&](int ps, float2 t) {
+    if (lane == 0) {
+      out_l[k][2 * ps] = t.x;
+      out_l[k][2 * ps + 1] = t.y;
     }
-    const ScaleSel sel(gl & 3);
-    down_passes<0>(wl, X, slo, shi, gl, hw, sel, out_l[k]);
-  }
+  };
+  if (k == K && wsh)
+    down_rows_q8<RPB / 2, DEC_DOWN_PF>(wsh, h16 + (size_t)K * F, r0, keep);
+  else if (k <= K)
+    down_rows<RPB / 2, DEC_DOWN_PF>(wq, k < K ? ids[k] : E, h16 + (size_t)k * F, r0, keep);
   __syncthreads();
   trace_point(trace, 2);
   if (threadIdx.x < RPB) {
