@@ -580,9 +580,13 @@ __global__ __launch_bounds__(MT_THREADS) void k_moe_mfma(
     const int32_t *__restrict__ n_tiles, int T, int K, __half *__restrict__ h16m,
     float *__restrict__ out) {
   using C = MfmaCfg<GATEUP>;
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  // The grid is sized for the most tiles T tokens can make; the blocks past
+  // this forward's work leave at once, and the work items are dealt over the
+  // real blocks only, so that every XCD gets an even share.
+  const int nreal = *n_tiles * C::NRT;
+  if ((int)blockIdx.x >= nreal) return;
+  const int w = xcd_remap(blockIdx.x, nreal);
   const int tile = w / C::NRT, rt = w % C::NRT;
-  if (tile >= *n_tiles) return;
   const int4 td = tiles[tile];
   const int e = td.x, o = td.y, n = td.z;
   const int tid = threadIdx.x;
