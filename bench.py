@@ -49,6 +49,9 @@ def parse():
     p.add_argument("--shared-q8", action="store_true",
                    help="shared expert in hy3's Q8_0, the type real checkpoints carry "
                         "(the configs' default is Q4_K)")
+    p.add_argument("--read-ceiling", action="store_true",
+                   help="print the streaming-read rate at the decode and prefill launch sizes "
+                        "(the achievable reference for the roofline fractions) and exit")
     p.add_argument("--residual", action="store_true",
                    help="time hy3x_layer_forward_residual (x += attn_out fused in front of "
                         "the block, as add_rmsnorm_kernel + gpu_ffn_moe)")
@@ -265,6 +268,16 @@ def main():
     import torch
     if a.copy_calibration:
         copy_calibration(torch, a.copy_calibration, a.steps)
+        return
+    if a.read_ceiling:
+        import hy3_amd as H
+        torch.cuda.init()
+        pool = torch.empty(4 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        rows = []
+        for mb in (8, 16, 32, 56, 96, 256, 1024):
+            us = H.read_rate_us(pool.data_ptr(), pool.numel(), mb << 20)
+            rows.append({"MiB": mb, "us": round(us, 2), "GB_per_s": round((mb << 20) / us / 1e3, 1)})
+        print(json.dumps({"read_ceiling": rows, "pool": "4 GiB, rotating slots"}), flush=True)
         return
     import hy3_amd as H
     from hy3_amd import configs as C

@@ -61,6 +61,7 @@ _SIGS = {
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
     "hy3x_layer_time_stage": (I32, [P, I32, I32, P, ctypes.POINTER(ctypes.c_float)]),
+    "hy3x_diag_read_rate": (I32, [P, I64, I64, I32, P, ctypes.POINTER(ctypes.c_float)]),
     "hy3x_layer_set_timing": (I32, [P, I32]),
     "hy3x_layer_set_trace": (I32, [P, I32, P]),
     "hy3x_layer_stats": (I32, [P, ctypes.POINTER(U64), ctypes.POINTER(U64), I32]),
@@ -137,6 +138,13 @@ def gguf_check_layer(path, layer_index):
     t = I32()
     _check(lib().hy3x_gguf_check_layer(os.fsencode(path), layer_index, ctypes.byref(t)))
     return t.value
+
+
+def read_rate_us(pool_ptr, pool_bytes, nbytes, reps=200, stream=None):
+    """Mean µs per launch of a plain streaming read of nbytes (hy3x_diag_read_rate)."""
+    us = ctypes.c_float()
+    _check(lib().hy3x_diag_read_rate(pool_ptr, pool_bytes, nbytes, reps, stream, ctypes.byref(us)))
+    return us.value
 
 
 class MoELayer:

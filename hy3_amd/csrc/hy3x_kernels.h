@@ -48,6 +48,7 @@ __global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_
                               const float *w, int K, float *x, const float *xadd,
                               const uint8_t *wsh,
                               unsigned long long *trace);
+__global__ void k_stream_read(const uint4 *p, int64_t n16, uint32_t *sink);
 __global__ void k_repack_q8x128(const uint8_t *src, uint8_t *dst, int64_t n_super);
 __global__ void k_synth_q8_0(uint8_t *dst, int64_t nblocks, uint64_t key, const float *src);
 __global__ void k_combine(float *x, const float *xadd, const float *out, const float *w, int T,

@@ -537,4 +537,34 @@ int hy3x_synth_quantize_q4k(const float *src, void *dst, int64_t n, void *stream
   return HY3X_OK;
 }
 
+int hy3x_diag_read_rate(const void *pool, int64_t pool_bytes, int64_t bytes, int reps,
+                        void *stream, float *us) {
+  if (!pool || !us || bytes < 16 || bytes % 16 || pool_bytes < bytes || reps < 1)
+    return fail(HY3X_E_ARG, "bad read-rate arguments");
+  hipStream_t st = (hipStream_t)stream;
+  uint32_t *sink = nullptr;
+  HIP_TRY(hipMalloc(&sink, 64));
+  const int64_t slots = pool_bytes / bytes, n16 = bytes / 16;
+  const unsigned grid = 2048;
+  auto launch = [&](int i) {
+    const uint4 *p = (const uint4 *)((const uint8_t *)pool + (i % slots) * bytes);
+    k_stream_read<<<grid, 256, 0, st>>>(p, n16, sink);
+  };
+  for (int i = 0; i < 10; i++) launch(i);
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipEventRecord(e0, st));
+  for (int i = 0; i < reps; i++) launch(i);
+  HIP_TRY(hipEventRecord(e1, st));
+  HIP_TRY(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipFree(sink);
+  *us = ms * 1e3f / reps;
+  return HY3X_OK;
+}
+
 }  // extern "C"

@@ -204,6 +204,25 @@ __global__ __launch_bounds__(256) void k_synth_q8_0(uint8_t *__restrict__ dst, i
   }
 }
 
+// Diagnostics: a plain streaming read of n16 16-byte words (a grid-stride
+// loop, eight loads in flight per thread), the reference point for what a
+// launch reading that many bytes can achieve. The XOR of the data is kept
+// live through a store that never happens for real inputs.
+__global__ __launch_bounds__(256) void k_stream_read(const uint4 *__restrict__ p, int64_t n16,
+                                                     uint32_t *__restrict__ sink) {
+  int64_t i = (int64_t)blockIdx.x * 256 * 8 + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  uint32_t acc = 0;
+  for (; i < n16; i += stride) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = i + 256 * u < n16 ? p[i + 256 * u] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
 }  // namespace hy3x
 
 using namespace hy3x;

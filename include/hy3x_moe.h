@@ -168,6 +168,15 @@ int hy3x_layer_stage_times(hy3x_layer *layer, float *ms, int n_stages, int *n_fo
  * is modified. No reference counterpart (measurement only). */
 int hy3x_layer_time_stage(hy3x_layer *layer, int stage, int reps, void *stream, float *us);
 
+/* Diagnostics: the reference point for the roofline fractions. Mean
+ * microseconds per launch of a plain streaming-read kernel reading `bytes`
+ * (multiple of 16) from the device buffer `pool`, successive launches taking
+ * successive `bytes`-sized slots of the pool so that a pool larger than the
+ * last-level cache defeats reuse; reps launches back to back between two HIP
+ * events (synchronises). No reference counterpart (measurement only). */
+int hy3x_diag_read_rate(const void *pool, int64_t pool_bytes, int64_t bytes, int reps,
+                        void *stream, float *us);
+
 /* Device-side counters since the last reset: forwards run and the sum over
  * forwards of the experts touched (shared expert included), i.e. the "U" of
  * the algorithmic byte count. Synchronises the device. */
