@@ -19,6 +19,7 @@ Prints ONE JSON line (rank 0). Fields beyond the driver's contract:
                 is absent, the oracle port, on a bounded token sample
 """
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -44,8 +45,11 @@ def parse():
     p.add_argument("--secondary", action="store_true", help="also measure the other configs")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--path", type=int, default=0, choices=(0, 1, 2),
-                   help="expert path: 0 the library's choice by T, 1 GEMV tiles, 2 MFMA tiles")
+    p.add_argument("--path", type=int, default=0, choices=(0, 1, 2, 3, 4),
+                   help="expert path: 0 the library's choice by T, 1 GEMV tiles, 2 MFMA tiles, "
+                        "3 / 4 MFMA with the narrow (32-token) / wide (64-token) tile shape")
+    p.add_argument("--tokens", type=int, default=0,
+                   help="override the config's token count (tuning sweeps)")
     p.add_argument("--shared-q8", action="store_true",
                    help="shared expert in hy3's Q8_0, the type real checkpoints carry "
                         "(the configs' default is Q4_K)")
@@ -124,7 +128,7 @@ def dominant_kernel(stage, T, path):
     """Kernel name of a stage on the path the library picks for T tokens."""
     if T == 1 and path == 0:
         return {"gateup": "k_gateup_decode", "down": "k_down_decode"}[stage]
-    mfma = path == 2 or (path == 0 and T >= 2)
+    mfma = path >= 2 or (path == 0 and T >= 2)
     if mfma:
         return {"gateup": "k_moe_mfma<true>", "down": "k_moe_mfma<false>"}[stage]
     return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
@@ -283,6 +287,8 @@ def main():
     from hy3_amd import configs as C
     torch.cuda.init()
     cfg = C.CONFIGS[a.config]
+    if a.tokens:
+        cfg = dataclasses.replace(cfg, T=a.tokens, name=f"{cfg.name}@T{a.tokens}")
     steps = a.steps or default_steps(cfg.T, cfg.n_layers)
     r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph, path=a.path,
                 shared_q8=a.shared_q8, residual=a.residual)
@@ -299,7 +305,7 @@ def main():
                    "layers": cfg.n_layers, "top_k": cfg.K, "experts": "192+1 shared",
                    "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu",
                    "launch": "hip-graph" if a.graph else "direct",
-                   "expert_path": ["auto", "gemv", "mfma"][a.path],
+                   "expert_path": ["auto", "gemv", "mfma", "mfma-narrow", "mfma-wide"][a.path],
                    "shared_expert": "q8_0" if a.shared_q8 else "q4_k",
                    "entry": "forward_residual" if a.residual else "forward"},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),

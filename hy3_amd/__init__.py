@@ -206,7 +206,7 @@ class MoELayer:
     def synth_shared_q8_0(self, seed, layer_index=0):
         _check(lib().hy3x_synth_shared_q8_0(self._h, seed, layer_index))
 
-    path = 0  # 0 auto, 1 GEMV, 2 MFMA (hy3x_layer_set_path)
+    path = 0  # 0 auto, 1 GEMV, 2 MFMA, 3 MFMA narrow, 4 MFMA wide (hy3x_layer_set_path)
 
     def set_path(self, path):
         _check(lib().hy3x_layer_set_path(self._h, path))

@@ -65,24 +65,31 @@ extern template __global__ void k_down_gemv<1>(const uint8_t *, const __half *, 
 extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, const int32_t *,
                                                const int4 *, const int32_t *, float *);
 
-// Waves per workgroup of the MFMA grouped GEMMs: a tile has 16 MFMA_WAVES
-// gate/up rows (per matrix) or 32 MFMA_WAVES down rows.
-#ifndef HY3X_MFMA_WAVES
-#define HY3X_MFMA_WAVES 4
-#endif
-constexpr int MFMA_WAVES = HY3X_MFMA_WAVES;
-template <bool GATEUP>
-__global__ __launch_bounds__(64 * MFMA_WAVES) void k_moe_mfma(
-    const uint8_t *wq, const uint8_t *wsh, const __half *act, const __half *act_sum,
-    const int32_t *list, const int4 *tiles, const int32_t *n_tiles, int T, int K,
-    __half *h16m, float *out);
-extern template __global__ void k_moe_mfma<true>(const uint8_t *, const uint8_t *, const __half *,
-                                                 const __half *, const int32_t *, const int4 *,
-                                                 const int32_t *, int, int, __half *, float *);
-extern template __global__ void k_moe_mfma<false>(const uint8_t *, const uint8_t *,
-                                                  const __half *, const __half *,
-                                                  const int32_t *, const int4 *, const int32_t *,
-                                                  int, int, __half *, float *);
+// The MFMA grouped GEMMs in two shapes (hy3x_mfma.hip, compiled once per
+// shape). A work tile has 16 WAVES gate/up rows (per matrix) or 32 WAVES down
+// rows and up to TOKENS tokens:
+//   narrow: 32 tokens, 4 waves -- two workgroups per CU; the shape for few
+//           tokens per expert;
+//   wide:   64 tokens, 8 waves -- one workgroup per CU, half the per-token
+//           dequantisation work; the shape for long prefills.
+#define HY3X_DECLARE_MFMA(NS, TOK, WV)                                                        \
+  namespace NS {                                                                            \
+  constexpr int TOKENS = TOK, WAVES = WV;                                                   \
+  template <bool GATEUP>                                                                    \
+  __global__ __launch_bounds__(64 * WV) void k_moe_mfma(                                    \
+      const uint8_t *wq, const uint8_t *wsh, const __half *act, const __half *act_sum,      \
+      const int32_t *list, const int4 *tiles, const int32_t *n_tiles, int T, int K,         \
+      __half *h16m, float *out);                                                            \
+  extern template __global__ void k_moe_mfma<true>(                                         \
+      const uint8_t *, const uint8_t *, const __half *, const __half *, const int32_t *,    \
+      const int4 *, const int32_t *, int, int, __half *, float *);                          \
+  extern template __global__ void k_moe_mfma<false>(                                        \
+      const uint8_t *, const uint8_t *, const __half *, const __half *, const int32_t *,    \
+      const int4 *, const int32_t *, int, int, __half *, float *);                          \
+  }
+HY3X_DECLARE_MFMA(mfma_narrow, 32, 4)
+HY3X_DECLARE_MFMA(mfma_wide, 64, 8)
+#undef HY3X_DECLARE_MFMA
 __global__ void k_stage_mfma(const float *s32, __half *s16m, __half *ssum);
 __global__ void k_hsums(const __half *h16m, __half *hsum);
 

@@ -51,6 +51,7 @@ struct hy3x_layer {
     int T = 0, K = 0, nt = 4, mt = 0;
     float scale = 1.0f;
     Mode mode = Mode::GEMV;
+    bool wide = false;  // MFMA mode: the wide tile shape (mfma_wide)
   } cur;
   hipStream_t last_stream = nullptr;
   int path = 0;
@@ -113,7 +114,10 @@ static int dalloc(P **p, size_t bytes) {
 
 // Up to this many tokens the router runs as one wave per (expert, token);
 // above it as RMSNorm + LDS-tiled GEMM + per-token top-K.
-constexpr int kSmallRouterT = 8;
+#ifndef HY3X_SMALL_ROUTER_T
+#define HY3X_SMALL_ROUTER_T 8
+#endif
+constexpr int kSmallRouterT = HY3X_SMALL_ROUTER_T;
 // Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks).
 constexpr int kMidRouterT = 128;
 // Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
@@ -123,6 +127,15 @@ constexpr int kLargeRouterT = 512;
 // T=32: 442 vs 550 us for gate/up + down), so the GEMV tiles only run when selected
 // explicitly (hy3x_layer_set_path 1); T = 1 keeps the fused decode kernels.
 constexpr int kMfmaMinT = 2;
+// From this many tokens the MFMA GEMMs use the wide tile shape (64 tokens, 8 waves).
+// Measured on MI355X (ms per layer, narrow vs wide): 32 tokens 0.32 vs 0.37,
+// 128: 0.43 vs 0.48, 256: 0.51 vs 0.56, 384: 0.60 vs 0.60, 512: 0.69 vs 0.65,
+// 4096 (Zipf routing): 3.36 vs 2.62 -- with few tokens per expert the tiles are
+// mostly empty and one workgroup per CU hides less latency than two.
+#ifndef HY3X_MFMA_WIDE_MIN_T
+#define HY3X_MFMA_WIDE_MIN_T 384
+#endif
+constexpr int kMfmaWideMinT = HY3X_MFMA_WIDE_MIN_T;
 
 static int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
@@ -276,7 +289,7 @@ int hy3x_layer_set_shared_q8_0(hy3x_layer *L, const void *gate, const void *up, 
 }
 
 int hy3x_layer_set_path(hy3x_layer *L, int path) {
-  if (!L || path < 0 || path > 2) return fail(HY3X_E_ARG, "bad path");
+  if (!L || path < 0 || path > 4) return fail(HY3X_E_ARG, "bad path");
   L->path = path;
   return HY3X_OK;
 }
@@ -333,10 +346,16 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         k_gateup_decode<<<K * DEC_GU_BLOCKS, 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
                                                           c.scale, L->ids, L->wpre, L->w,
                                                           L->stats, L->h16, L->trace[1]);
+      else if (c.mode == Mode::MFMA && c.wide)
+        mfma_wide::k_moe_mfma<true>
+            <<<mt * (F / (16 * mfma_wide::WAVES)), 64 * mfma_wide::WAVES, 0, st>>>(
+                L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list, L->tiles,
+                L->n_tiles, T, K, L->h16m, nullptr);
       else if (c.mode == Mode::MFMA)
-        k_moe_mfma<true><<<mt * (F / (16 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list,
-                                                        L->tiles, L->n_tiles, T, K, L->h16m,
-                                                        nullptr);
+        mfma_narrow::k_moe_mfma<true>
+            <<<mt * (F / (16 * mfma_narrow::WAVES)), 64 * mfma_narrow::WAVES, 0, st>>>(
+                L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list, L->tiles,
+                L->n_tiles, T, K, L->h16m, nullptr);
       else
         k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles,
                                                         L->n_tiles, T, K, L->h16);
@@ -348,9 +367,17 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
             L->trace[2]);
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
-        k_moe_mfma<false><<<mt * (D / (32 * MFMA_WAVES)), 64 * MFMA_WAVES, 0, st>>>(L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16m, L->hsum, L->list,
-                                                          L->tiles, L->n_tiles, T, K, nullptr,
-                                                          L->out);
+        const uint8_t *wsh = L->shared_q8 ? L->wsh : nullptr;
+        if (c.wide)
+          mfma_wide::k_moe_mfma<false>
+              <<<mt * (D / (32 * mfma_wide::WAVES)), 64 * mfma_wide::WAVES, 0, st>>>(
+                  L->wq, wsh, L->h16m, L->hsum, L->list, L->tiles, L->n_tiles, T, K, nullptr,
+                  L->out);
+        else
+          mfma_narrow::k_moe_mfma<false>
+              <<<mt * (D / (32 * mfma_narrow::WAVES)), 64 * mfma_narrow::WAVES, 0, st>>>(
+                  L->wq, wsh, L->h16m, L->hsum, L->list, L->tiles, L->n_tiles, T, K, nullptr,
+                  L->out);
       }
       else
         k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles,
@@ -391,13 +418,16 @@ static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K
   c.scale = scale;
   if (T == 1 && L->path == 0)
     c.mode = Mode::DECODE;
-  else if (L->path == 2 || (L->path == 0 && T >= kMfmaMinT))
+  else if (L->path >= 2 || (L->path == 0 && T >= kMfmaMinT))
     c.mode = Mode::MFMA;
   else
     c.mode = Mode::GEMV;
   if (L->shared_q8 && c.mode == Mode::GEMV)
     return fail(HY3X_E_STATE, "the GEMV tile path needs a Q4_K shared expert");
-  c.nt = c.mode == Mode::MFMA ? 32 : 4;  // tokens per work tile
+  c.wide = c.mode == Mode::MFMA &&
+           (L->path == 4 || (L->path != 3 && T >= kMfmaWideMinT));
+  // tokens per work tile
+  c.nt = c.mode != Mode::MFMA ? 4 : c.wide ? mfma_wide::TOKENS : mfma_narrow::TOKENS;
   c.mt = std::min(max_tiles_for(T, K, c.nt), L->max_tiles_alloc);
   record_stage(L, st, -1);
   for (int stage = HY3X_STAGE_ROUTER; stage <= HY3X_STAGE_COMBINE; stage++) {

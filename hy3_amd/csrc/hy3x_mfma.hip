@@ -1,9 +1,9 @@
 // hy3x_mfma.hip -- grouped Q4_K x fp16 GEMMs on the matrix cores (prefill).
 //
-// A work tile is one expert, a slice of its weight matrix -- 16 MFMA_WAVES
-// rows of gate and of up, or 32 MFMA_WAVES rows of down (each wave 16 or
-// 2 x 16 rows) -- and up to 32 of its tokens (the dispatch tile list with
-// NT = 32).
+// A work tile is one expert, a slice of its weight matrix -- 16 WAVES
+// rows of gate and of up, or 32 WAVES rows of down (each wave 16 or
+// 2 x 16 rows) -- and up to TOKENS (32 or 64) of its tokens (the dispatch
+// tile list with NT = TOKENS), in 16-token MFMA column groups (NTT of them).
 //
 // Per Q4_K block column (256 of K):
 //  * the tile's 256 row-blocks (144 B each) are copied from HBM straight into
@@ -49,8 +49,17 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));  // 16 bytes as a native vector
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
-constexpr int MT_TOK = 32;                 // tokens per tile (dispatch NT for this path)
-constexpr int MT_WAVES = MFMA_WAVES;       // waves per workgroup
+// This file is compiled twice: as the narrow shape (namespace mfma_narrow)
+// and, with HY3X_MFMA_WIDE defined (hy3x_mfma_wide.hip), as the wide one.
+#ifdef HY3X_MFMA_WIDE
+namespace mfma_wide {
+#else
+namespace mfma_narrow {
+#endif
+
+constexpr int MT_TOK = TOKENS;             // tokens per tile (dispatch NT for this path)
+static_assert(MT_TOK == 32 || MT_TOK == 64, "tile tokens");
+constexpr int MT_WAVES = WAVES;            // waves per workgroup
 constexpr int MT_THREADS = 64 * MT_WAVES;
 constexpr int RB = 32 * MT_WAVES;          // row-blocks per tile and block column
 constexpr int RB_HALF = 16 * MT_WAVES;     // gate/up: gate row-blocks, then up
@@ -417,7 +426,7 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
 // 144-byte super-block per row = 128 k = four 32-weight blocks, each exactly
 // one 16x16x32 MFMA, so the weight copies are the Q4_K path's (issue_a).
 // Activations: 16 chunks per token per column in bt_st[buf] viewed as
-// [32 tokens][16 chunks], chunk c of row r at position c ^ (r & 15). The
+// [MT_TOK tokens][16 chunks], chunk c of row r at position c ^ (r & 15). The
 // weights are the exact integers q in fp16 ((1152 + q) from the byte
 // permute, minus 1152) and each block's MFMA result is scaled by its d in
 // fp32: acc += d_b * (x_b . q_b) -- sum d*q*x as mul_mat_f32 case 8
@@ -566,7 +575,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return x * q + (x < r ? x : r) + i;
 }
 
-// Grouped GEMM over the tile list (tiles of at most 32 tokens). GATEUP:
+// Grouped GEMM over the tile list (tiles of at most MT_TOK tokens). GATEUP:
 // weights = gate and up rows of the expert (K = 4096), activations = staged
 // s, epilogue h = silu(g) * u -> h16m[slot][perm8(row)] (fp16). Otherwise
 // weights = down rows (K = 1536), activations = h16m, out[slot][row] fp32.
@@ -598,16 +607,48 @@ __global__ __launch_bounds__(MT_THREADS) void k_moe_mfma(
   }
   __syncthreads();
   if (wsh && e == E) {
+    if constexpr (MT_TOK > 32) {
+      if (n > 48) {
+        mfma_tile_q8<GATEUP, 4>(wsh, act, n, rt, h16m, out);
+        return;
+      }
+      if (n > 32) {
+        mfma_tile_q8<GATEUP, 3>(wsh, act, n, rt, h16m, out);
+        return;
+      }
+    }
     if (n > 16)
       mfma_tile_q8<GATEUP, 2>(wsh, act, n, rt, h16m, out);
     else
       mfma_tile_q8<GATEUP, 1>(wsh, act, n, rt, h16m, out);
-  } else if (n > 16) {
-    mfma_tile<GATEUP, 2>(wq, act, act_sum, e, n, rt, h16m, out);
-  } else {
-    mfma_tile<GATEUP, 1>(wq, act, act_sum, e, n, rt, h16m, out);
+    return;
   }
+  if constexpr (MT_TOK > 32) {
+    if (n > 48) {
+      mfma_tile<GATEUP, 4>(wq, act, act_sum, e, n, rt, h16m, out);
+      return;
+    }
+    if (n > 32) {
+      mfma_tile<GATEUP, 3>(wq, act, act_sum, e, n, rt, h16m, out);
+      return;
+    }
+  }
+  if (n > 16)
+    mfma_tile<GATEUP, 2>(wq, act, act_sum, e, n, rt, h16m, out);
+  else
+    mfma_tile<GATEUP, 1>(wq, act, act_sum, e, n, rt, h16m, out);
 }
+
+template __global__ void k_moe_mfma<true>(const uint8_t *, const uint8_t *, const __half *,
+                                          const __half *, const int32_t *, const int4 *,
+                                          const int32_t *, int, int, __half *, float *);
+template __global__ void k_moe_mfma<false>(const uint8_t *, const uint8_t *, const __half *,
+                                           const __half *, const int32_t *, const int4 *,
+                                           const int32_t *, int, int, __half *, float *);
+
+}  // namespace mfma_narrow / mfma_wide
+
+#ifndef HY3X_MFMA_WIDE
 
 // fp16 copy of s in the MFMA run order (perm8) for the gate/up activations,
 // and its 128 sub-block sums.
@@ -628,11 +669,6 @@ __global__ __launch_bounds__(64) void k_hsums(const __half *__restrict__ h16m,
   row_subsums(h16m + (size_t)slot * F, F / 32, hsum + (size_t)slot * (F / 32) * 4);
 }
 
-template __global__ void k_moe_mfma<true>(const uint8_t *, const uint8_t *, const __half *,
-                                          const __half *, const int32_t *, const int4 *,
-                                          const int32_t *, int, int, __half *, float *);
-template __global__ void k_moe_mfma<false>(const uint8_t *, const uint8_t *, const __half *,
-                                           const __half *, const int32_t *, const int4 *,
-                                           const int32_t *, int, int, __half *, float *);
+#endif  // !HY3X_MFMA_WIDE
 
 }  // namespace hy3x

@@ -189,7 +189,9 @@ int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_to
 int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
 
 /* Execution-path override for tests: 0 = automatic (by T), 1 = force the
- * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path. */
+ * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path (tile
+ * shape by T), 3 = MFMA with the narrow tile shape (32 tokens), 4 = MFMA with
+ * the wide tile shape (64 tokens). */
 int hy3x_layer_set_path(hy3x_layer *layer, int path);
 
 /* ---- synthetic inputs (test / benchmark data, not part of the MoE path) ----

@@ -283,19 +283,54 @@ def test_routing_with_ties(torch, T, case):
 
 @pytest.mark.parametrize("T", [1, 7, 64, 200])
 def test_expert_paths_match_oracle(torch, layer, cpu, T):
-    """Every expert path (0 automatic, 1 wavefront GEMV, 2 MFMA grouped GEMM)
-    meets the tolerance on the same tokens; routing is identical on all."""
+    """Every expert path (0 automatic, 1 wavefront GEMV, 2 MFMA grouped GEMM,
+    3 / 4 its narrow / wide tile shape) meets the tolerance on the same
+    tokens; routing is identical on all."""
     x = C.inputs(0xC2, T, first_token=300)
     rows = np.linspace(0, T - 1, min(T, 6)).astype(int)
     yo, ro = cpu.forward(x[rows])
     try:
-        for path in (0, 1, 2):
+        for path in (0, 1, 2, 3, 4):
             layer.set_path(path)
             y, ids, _, _ = run(torch, layer, x)
             assert np.array_equal(ids[rows], ro["ids"]), path
             assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL, path
     finally:
         layer.set_path(0)
+
+
+@pytest.mark.parametrize("T", [40, 200])
+def test_mfma_tile_shapes_on_crowded_experts(torch, layer, cpu, T):
+    """A bias of +50 on eight experts sends every token to them, so each of
+    those experts holds all T tokens: the narrow shape (32-token tiles) and the
+    wide one (64-token tiles: T = 40 is one tile of 40 tokens, three 16-token
+    column groups; T = 200 is three full tiles of four groups and one of 8
+    tokens) agree to 1e-6 relative (the same integer MFMA sums; the two
+    shapes' compiled epilogues may round a gate/up value a last bit apart,
+    which moves that token's fp16 h by one step) and meet the oracle's
+    tolerance."""
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    hot = np.array([5, 17, 60, 61, 99, 130, 171, 191])
+    b = b.copy()
+    b[hot] = 50.0
+    layer.set_router(nw, rt, b)
+    saved = cpu.bias
+    cpu.bias = b
+    x = C.inputs(0xC5, T)
+    try:
+        out = {}
+        for path in (3, 4):
+            layer.set_path(path)
+            out[path], ids, _, _ = run(torch, layer, x)
+            assert np.array_equal(np.sort(ids, axis=1), np.tile(np.sort(hot), (T, 1)))
+        assert O.rel_l2(out[3] - x, out[4] - x) <= 1e-6
+        rows = np.linspace(0, T - 1, 5).astype(int)
+        yo, _ = cpu.forward(x[rows])
+        assert O.rel_l2(out[4][rows] - x[rows], yo - x[rows]) <= TOL
+    finally:
+        layer.set_path(0)
+        layer.set_router(nw, rt, C.layer_small_tensors(C.WEIGHT_SEED)[2])
+        cpu.bias = saved
 
 
 @pytest.mark.parametrize("T", [1, 64])
@@ -397,13 +432,18 @@ def test_q4k_shared_restored_after_q8(torch, layer, cpu):
     assert O.rel_l2(y - x, yo - x) <= TOL
 
 
-@pytest.mark.parametrize("T", [2, 40])
-def test_q8_shared_mfma_matches_oracle(torch, q8_layer, cpu, q8_mats, T):
+@pytest.mark.parametrize("T,path", [(2, 0), (40, 3), (40, 4), (64, 4)])
+def test_q8_shared_mfma_matches_oracle(torch, q8_layer, cpu, q8_mats, T, path):
     """T >= 2 with hy3's Q8_0 shared expert: the MFMA grouped GEMM runs the
-    shared expert's tiles from its Q8 matrices (T = 40: one tile of 32 tokens
-    and one of 8)."""
+    shared expert's tiles from its Q8 matrices (T = 40, narrow shape: one tile
+    of 32 tokens and one of 8; wide shape: one tile of 40, three 16-token
+    column groups; T = 64: one full wide tile)."""
     x = O.normal(T * D, O.key(0xC1, 0, O.T_X), 1.0).reshape(T, D)
-    y, ids, wpre, w = run(torch, q8_layer, x)
+    q8_layer.set_path(path)
+    try:
+        y, ids, wpre, w = run(torch, q8_layer, x)
+    finally:
+        q8_layer.set_path(0)
     yo, ro = q8_oracle(cpu, q8_mats, ids).forward(x)
     assert np.array_equal(ids, ro["ids"])
     assert O.rel_l2(y - x, yo - x) <= TOL
