@@ -127,16 +127,13 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v));
 // Four elements of the residual stream x, plus the addend xadd when the
 // forward carries one (x + attn_out, the residual add of hy3.c:1264 and of
 // add_rmsnorm_kernel, hy3_gpu.cu:453-460; the same fp32 add in every reader).
+// Branch-free, so that a caller's other loads stay in flight: without an
+// addend the second load re-reads x (a cache hit) and its sum is discarded.
 __device__ __forceinline__ float4 load_x4(const float *x, const float *xadd, size_t i4) {
-  float4 v = reinterpret_cast<const float4 *>(x)[i4];
-  if (xadd) {
-    const float4 a = reinterpret_cast<const float4 *>(xadd)[i4];
-    v.x = v.x + a.x;
-    v.y = v.y + a.y;
-    v.z = v.z + a.z;
-    v.w = v.w + a.w;
-  }
-  return v;
+  const float4 v = reinterpret_cast<const float4 *>(x)[i4];
+  const float4 a = reinterpret_cast<const float4 *>(xadd ? xadd : x)[i4];
+  const float4 s = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+  return xadd ? s : v;
 }
 
 }  // namespace hy3x

@@ -12,15 +12,22 @@ namespace hy3x {
 // row dot with DPP and lane 0 writes h = silu(g) * u, pair-staged, to
 // h16[slot * F + ...] (hy3.c:1296-1300 / 1307-1314).
 template <int RPW, int PF>
-__device__ __forceinline__ void gateup_rows(const uint8_t *__restrict__ wq, int e, int slot,
-                                            int r0, const uint32_t (&X)[32], float slo,
-                                            float shi, __half *__restrict__ h16) {
-  const int lane = threadIdx.x & 63, b = lane >> 2, p = lane & 3;
-  const ScaleSel sel(p);
-  const uint8_t *gbase = wq + (size_t)e * EXPERT_BYTES + (size_t)b * QB;
-  const uint8_t *ubase = gbase + MAT_BYTES;
+struct GateupRows {
+  // Split in two so that a caller can put the first PF rows' loads in flight
+  // before it has the activations (the constructor issues them).
   uint4 ring[PF][6];
-  auto issue = [&](int rr, uint4 (&dst)[6]) {
+  const uint8_t *gbase, *ubase;
+  int slot, r0;
+  __device__ __forceinline__ GateupRows(const uint8_t *__restrict__ wq, int e, int slot_, int r0_)
+      : slot(slot_), r0(r0_) {
+    const int lane = threadIdx.x & 63, b = lane >> 2;
+    gbase = wq + (size_t)e * EXPERT_BYTES + (size_t)b * QB;
+    ubase = gbase + MAT_BYTES;
+#pragma unroll
+    for (int rr = 0; rr < PF && rr < RPW; rr++) issue(rr, ring[rr]);
+  }
+  __device__ __forceinline__ void issue(int rr, uint4 (&dst)[6]) const {
+    const int p = threadIdx.x & 3;
     const uint8_t *gp = gbase + (size_t)(r0 + rr) * (D / QK) * QB;
     const uint8_t *up = ubase + (size_t)(r0 + rr) * (D / QK) * QB;
     dst[0] = *reinterpret_cast<const uint4 *>(gp);
@@ -29,23 +36,34 @@ __device__ __forceinline__ void gateup_rows(const uint8_t *__restrict__ wq, int 
     dst[3] = *reinterpret_cast<const uint4 *>(up);
     dst[4] = *reinterpret_cast<const uint4 *>(up + 16 + 32 * p);
     dst[5] = *reinterpret_cast<const uint4 *>(up + 32 + 32 * p);
-  };
-#pragma unroll
-  for (int rr = 0; rr < PF && rr < RPW; rr++) issue(rr, ring[rr]);
-#pragma unroll
-  for (int rr = 0; rr < RPW; rr++) {
-    uint4 cur[6];
-#pragma unroll
-    for (int q = 0; q < 6; q++) cur[q] = ring[rr % PF][q];
-    if (rr + PF < RPW) issue(rr + PF, ring[rr % PF]);
-    uint32_t P[32];
-    unpack_group(cur[1], cur[2], P);
-    const float gv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
-    unpack_group(cur[4], cur[5], P);
-    const float uv = group_dot(P, X, slo, shi, block_scale(cur[3], sel));
-    const float g = wave_total(gv), u = wave_total(uv);
-    if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
   }
+  __device__ __forceinline__ void finish(const uint32_t (&X)[32], float slo, float shi,
+                                         __half *__restrict__ h16) {
+    const int lane = threadIdx.x & 63;
+    const ScaleSel sel(lane & 3);
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++) {
+      uint4 cur[6];
+#pragma unroll
+      for (int q = 0; q < 6; q++) cur[q] = ring[rr % PF][q];
+      if (rr + PF < RPW) issue(rr + PF, ring[rr % PF]);
+      uint32_t P[32];
+      unpack_group(cur[1], cur[2], P);
+      const float gv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
+      unpack_group(cur[4], cur[5], P);
+      const float uv = group_dot(P, X, slo, shi, block_scale(cur[3], sel));
+      const float g = wave_total(gv), u = wave_total(uv);
+      if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
+    }
+  }
+};
+
+template <int RPW, int PF>
+__device__ __forceinline__ void gateup_rows(const uint8_t *__restrict__ wq, int e, int slot,
+                                            int r0, const uint32_t (&X)[32], float slo,
+                                            float shi, __half *__restrict__ h16) {
+  GateupRows<RPW, PF> rows(wq, e, slot, r0);
+  rows.finish(X, slo, shi, h16);
 }
 
 // Down rows r0 .. r0 + 2 PASSES - 1 of expert e for one token, one wave:

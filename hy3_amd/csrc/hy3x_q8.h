@@ -86,26 +86,42 @@ __device__ __forceinline__ float q8_group_dot(const Q8Group &gq, const uint32_t 
 // one token, like gateup_rows: lane = 64-weight group, PF rows in flight,
 // h = silu(g) * u pair-staged into h16[slot * F + ...] (hy3.c:1296-1300).
 template <int RPW, int PF>
+struct GateupRowsQ8 {
+  // As GateupRows: the constructor puts the first PF rows' loads in flight.
+  static constexpr int ROWB = D / Q8K * QB;  // 4608 bytes per gate/up row
+  Q8Group ring[PF][2];
+  const uint8_t *wsh;
+  int slot, r0;
+  __device__ __forceinline__ GateupRowsQ8(const uint8_t *__restrict__ wsh_, int slot_, int r0_)
+      : wsh(wsh_), slot(slot_), r0(r0_) {
+#pragma unroll
+    for (int rr = 0; rr < PF && rr < RPW; rr++) issue(rr, ring[rr]);
+  }
+  __device__ __forceinline__ void issue(int rr, Q8Group (&dst)[2]) const {
+    const int lane = threadIdx.x & 63;
+    load_q8_group(wsh + (size_t)(r0 + rr) * ROWB, lane, dst[0]);
+    load_q8_group(wsh + Q8_MAT_BYTES + (size_t)(r0 + rr) * ROWB, lane, dst[1]);
+  }
+  __device__ __forceinline__ void finish(const uint32_t (&X)[32], float slo, float shi,
+                                         __half *__restrict__ h16) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++) {
+      Q8Group cur[2] = {ring[rr % PF][0], ring[rr % PF][1]};
+      if (rr + PF < RPW) issue(rr + PF, ring[rr % PF]);
+      const float g = wave_total(q8_group_dot(cur[0], X, slo, shi));
+      const float u = wave_total(q8_group_dot(cur[1], X, slo, shi));
+      if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
+    }
+  }
+};
+
+template <int RPW, int PF>
 __device__ __forceinline__ void gateup_rows_q8(const uint8_t *__restrict__ wsh, int slot, int r0,
                                                const uint32_t (&X)[32], float slo, float shi,
                                                __half *__restrict__ h16) {
-  const int lane = threadIdx.x & 63;
-  constexpr int ROWB = D / Q8K * QB;  // 4608 bytes per gate/up row
-  Q8Group ring[PF][2];
-  auto issue = [&](int rr, Q8Group (&dst)[2]) {
-    load_q8_group(wsh + (size_t)(r0 + rr) * ROWB, lane, dst[0]);
-    load_q8_group(wsh + Q8_MAT_BYTES + (size_t)(r0 + rr) * ROWB, lane, dst[1]);
-  };
-#pragma unroll
-  for (int rr = 0; rr < PF && rr < RPW; rr++) issue(rr, ring[rr]);
-#pragma unroll
-  for (int rr = 0; rr < RPW; rr++) {
-    Q8Group cur[2] = {ring[rr % PF][0], ring[rr % PF][1]};
-    if (rr + PF < RPW) issue(rr + PF, ring[rr % PF]);
-    const float g = wave_total(q8_group_dot(cur[0], X, slo, shi));
-    const float u = wave_total(q8_group_dot(cur[1], X, slo, shi));
-    if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
-  }
+  GateupRowsQ8<RPW, PF> rows(wsh, slot, r0);
+  rows.finish(X, slo, shi, h16);
 }
 
 // Down rows r0 .. r0 + 2 PASSES - 1 of the Q8 shared expert for one token,

@@ -158,35 +158,54 @@ __global__ __launch_bounds__(256) void k_route_decode(
                  s32, trace);
     return;
   }
-  // shared expert: s = rmsnorm(x) * norm_w, pair-staged fp16 in LDS
+  // shared expert: s = rmsnorm(x) * norm_w, pair-staged fp16 in LDS. The
+  // loads of x and norm_w go first, then the rows' weight loads (they need no
+  // s), so the weights stream in while the block reduces and stages s.
   trace_point(trace, 0);
   __shared__ __attribute__((aligned(16))) __half s_l[D];
   __shared__ float red_l[4];
   const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
-  float4 a[4];
+  float4 a[4], ad[4], w4[4];
 #pragma unroll
-  for (int u = 0; u < 4; u++) a[u] = load_x4(x, xadd, tid + 256 * u);
-  const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
-#pragma unroll
-  for (int u = 0; u < 4; u++) {
-    const float4 w = wg[tid + 256 * u];
-    const int j = 4 * (tid + 256 * u);
-    stage_store(s_l, j + 0, (a[u].x * w.x) * r);
-    stage_store(s_l, j + 1, (a[u].y * w.y) * r);
-    stage_store(s_l, j + 2, (a[u].z * w.z) * r);
-    stage_store(s_l, j + 3, (a[u].w * w.w) * r);
+  for (int u = 0; u < 4; u++) {  // x + xadd as load_x4, the add deferred
+    a[u] = reinterpret_cast<const float4 *>(x)[tid + 256 * u];
+    ad[u] = reinterpret_cast<const float4 *>(xadd ? xadd : x)[tid + 256 * u];
+    w4[u] = wg[tid + 256 * u];
   }
-  __syncthreads();
   const int lane = tid & 63, wave = tid >> 6, sb = blockIdx.x - E;
+  const int r0 = sb * DEC_RPB + wave * DEC_RPW;
+  auto stage_s = [&](uint32_t (&X)[32], float &slo, float &shi) {
+    if (xadd) {
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        a[u] = make_float4(a[u].x + ad[u].x, a[u].y + ad[u].y, a[u].z + ad[u].z,
+                           a[u].w + ad[u].w);
+    }
+    const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int j = 4 * (tid + 256 * u);
+      stage_store(s_l, j + 0, (a[u].x * w4[u].x) * r);
+      stage_store(s_l, j + 1, (a[u].y * w4[u].y) * r);
+      stage_store(s_l, j + 2, (a[u].z * w4[u].z) * r);
+      stage_store(s_l, j + 3, (a[u].w * w4[u].w) * r);
+    }
+    __syncthreads();
+    load_group_x(s_l, lane, X);
+    group_sums(X, slo, shi);
+    trace_point(trace, 1);
+  };
   uint32_t X[32];
-  load_group_x(s_l, lane, X);
   float slo, shi;
-  group_sums(X, slo, shi);
-  trace_point(trace, 1);
-  if (wsh)
-    gateup_rows_q8<DEC_RPW, 2>(wsh, K, sb * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
-  else
-    gateup_rows<DEC_RPW, DEC_RPW>(wq, E, K, sb * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
+  if (wsh) {
+    GateupRowsQ8<DEC_RPW, 2> rows(wsh, K, r0);
+    stage_s(X, slo, shi);
+    rows.finish(X, slo, shi, h16);
+  } else {
+    GateupRows<DEC_RPW, DEC_RPW> rows(wq, E, K, r0);
+    stage_s(X, slo, shi);
+    rows.finish(X, slo, shi, h16);
+  }
   trace_point(trace, 3);
 }
 
