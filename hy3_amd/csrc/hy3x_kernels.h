@@ -12,15 +12,30 @@ __global__ void k_router_logits(const float *x, const float *xadd, const float *
 __global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w, __half *s16,
                           float *s32,
                           __half *s16m, __half *ssum, int T, uint32_t *bits, int wt);
-template <int MT, int ME, int TG, int EG>
+// K chunk of the router GEMM: small and mid-size tiles (4 x 8 and 8 x 16
+// tokens x experts) and the larger ones. Tuning macros.
+#ifndef HY3X_ROUTER_KC_MID
+#define HY3X_ROUTER_KC_MID 256
+#endif
+#ifndef HY3X_ROUTER_KC_LARGE
+#define HY3X_ROUTER_KC_LARGE 128
+#endif
+constexpr int ROUTER_KC_MID = HY3X_ROUTER_KC_MID, ROUTER_KC_LARGE = HY3X_ROUTER_KC_LARGE;
+template <int MT, int ME, int TG, int EG, int KC>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
                                                      float *logits);
-extern template __global__ void k_router_gemm<4, 4, 4, 8>(const float *, const float *, int,
-                                                          float *);
-extern template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const float *, int,
-                                                          float *);
-extern template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int,
-                                                          float *);
+extern template __global__ void k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE>(const float *,
+                                                                           const float *, int,
+                                                                           float *);
+extern template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID>(const float *,
+                                                                         const float *, int,
+                                                                         float *);
+extern template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID>(const float *,
+                                                                         const float *, int,
+                                                                         float *);
+extern template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE>(const float *,
+                                                                           const float *, int,
+                                                                           float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
                        int T, int32_t *ids, float *wpre, float *wout, uint32_t *bits, int wt);
 __global__ void k_dispatch_list(const int32_t *ids, int T, int K, int NT, const uint32_t *bits,

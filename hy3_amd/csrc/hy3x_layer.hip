@@ -118,6 +118,12 @@ static int dalloc(P **p, size_t bytes) {
 #define HY3X_SMALL_ROUTER_T 8
 #endif
 constexpr int kSmallRouterT = HY3X_SMALL_ROUTER_T;
+// Up to this many tokens the router GEMM uses 4 x 8 block tiles, one output per thread
+// group (the most blocks: at T = 32, 192 of them).
+#ifndef HY3X_TINY_ROUTER_T
+#define HY3X_TINY_ROUTER_T 64
+#endif
+constexpr int kTinyRouterT = HY3X_TINY_ROUTER_T;
 // Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks).
 constexpr int kMidRouterT = 128;
 // Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
@@ -319,14 +325,17 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         const bool mf = c.mode == Mode::MFMA;
         k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : L->s16, L->s32,
                                      mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt);
-        if (T <= kMidRouterT)
-          k_router_gemm<2, 2, 4, 8><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
+        if (T <= kTinyRouterT)
+          k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
+              L->s32, L->router, T, L->logits);
+        else if (T <= kMidRouterT)
+          k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else if (T <= kLargeRouterT)
-          k_router_gemm<4, 4, 4, 8><<<dim3((T + 15) / 16, E / 32), 256, 0, st>>>(
+          k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE><<<dim3((T + 15) / 16, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else
-          k_router_gemm<8, 4, 4, 8><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
+          k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
       }
       k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, T, L->ids,

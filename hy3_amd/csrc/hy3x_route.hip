@@ -20,6 +20,7 @@
 // fp32 division and sqrt are correctly rounded (built with
 // -fhip-fp32-correctly-rounded-divide-sqrt) and nothing in this file is
 // contracted into FMAs beyond the explicit fmaf calls.
+#include "hy3x_kernels.h"
 #include "hy3x_route.h"
 #include "hy3x_decode.h"
 #include "hy3x_q8.h"
@@ -265,13 +266,16 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
 // micro-tile of (token, expert) outputs; the 8 chains of a micro-tile sit in
 // 8 neighbouring lanes and are combined with tree8_lanes. Block tile:
 // TT = MT*TG tokens x TE = ME*EG experts, K walked in chunks of KC staged
-// k-major in LDS (double-buffered, next chunk prefetched into registers).
-template <int MT, int ME, int TG, int EG>
+// k-major in LDS (double-buffered, next chunk prefetched into registers). The
+// chunk is large (few blocks run at small T, so each K step's load latency is
+// paid in sequence: the fewer steps, the better).
+template <int MT, int ME, int TG, int EG, int KC>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s32,
                                                      const float *__restrict__ router, int T,
                                                      float *__restrict__ logits) {
   static_assert(8 * TG * EG == 256, "256 threads");
-  constexpr int TT = MT * TG, TE = ME * EG, KC = 128;
+  static_assert(D % KC == 0 && KC % 8 == 0, "K chunks");
+  constexpr int TT = MT * TG, TE = ME * EG;
   constexpr int SP = TT + 4, WP = TE + 4;        // padded LDS rows (floats)
   constexpr int NS = TT * KC / 4 / 256, NW = TE * KC / 4 / 256;  // float4 per thread
   static_assert(NS >= 1 && NW >= 1, "staging split");
@@ -344,9 +348,14 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
       if (v == 0 && tt < T) logits[(size_t)tt * E + ee] = lg;
     }
 }
-template __global__ void k_router_gemm<4, 4, 4, 8>(const float *, const float *, int, float *);
-template __global__ void k_router_gemm<8, 4, 4, 8>(const float *, const float *, int, float *);
-template __global__ void k_router_gemm<2, 2, 4, 8>(const float *, const float *, int, float *);
+template __global__ void k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE>(const float *, const float *,
+                                                                    int, float *);
+template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE>(const float *, const float *,
+                                                                    int, float *);
+template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID>(const float *, const float *,
+                                                                  int, float *);
+template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID>(const float *, const float *,
+                                                                  int, float *);
 
 // Routing of one token per block (T > 1 paths): sigmoid and scores of the
 // 192 logits, then the top-K.
