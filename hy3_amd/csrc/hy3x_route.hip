@@ -464,9 +464,16 @@ __global__ __launch_bounds__(256) void k_dispatch_list(
       const int b = __ffs(word) - 1;
       word &= word - 1u;
       const int t = 32 * w + b;
-      int k = 0;
-      for (; k < K - 1; k++)
-        if (ids[(size_t)t * K + k] == e) break;
+      // the rank of e among t's ids (K - 1 when no earlier one matches): all
+      // loads issued at once, the first match kept
+      int idv[KMAX - 1];
+#pragma unroll
+      for (int kk = 0; kk < KMAX - 1; kk++)  // clamped: a valid address for any K
+        idv[kk] = ids[(size_t)t * K + (kk < K ? kk : K - 1)];
+      int k = K - 1;
+#pragma unroll
+      for (int kk = KMAX - 2; kk >= 0; kk--)
+        if (kk < K - 1 && idv[kk] == e) k = kk;
       list[eoff + pos + r] = t * K + k;
       r++;
     }
