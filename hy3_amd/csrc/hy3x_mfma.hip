@@ -191,7 +191,26 @@ struct TileState {
   const uint8_t *sbase;         // sums (uniform)
   uint32_t soff;                // sums chunk (lanes below S_LANES), from sbase
   f4_t acc[RG][NMAT][NTT];
+  // the last column's block sums and scales d, added to acc (acc += d * pend)
+  // in the next column, where the adds overlap that column's MFMAs
+  f4_t pend[RG][NMAT][NTT];
+  float pend_d[RG][NMAT];
 };
+
+// acc += d * Dblk of the previous column (zeros before the first).
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void apply_pending(TileState<GATEUP, NTT> &st) {
+#pragma unroll
+  for (int rg = 0; rg < TileState<GATEUP, NTT>::RG; rg++)
+#pragma unroll
+    for (int m = 0; m < TileState<GATEUP, NTT>::NMAT; m++)
+#pragma unroll
+      for (int t = 0; t < NTT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          st.acc[rg][m][t][i] = __builtin_fmaf(st.pend_d[rg][m], st.pend[rg][m][t][i],
+                                               st.acc[rg][m][t][i]);
+}
 
 // Copies of column kb: activations and sums into buffer kb & 1, then weights
 // of column ka into ring stage ka % 3 -- always B_DMA + 1 + A_DMA copies per
@@ -274,6 +293,9 @@ __device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
     sv[t] = __builtin_bit_cast(h8_t, bm_st[buf][16 * t + lr][g ^ ((lr >> 2) & 3)]);
   }
 
+  // the previous column's d * Dblk, in the same order on acc as if it had
+  // been added there (mins MFMA of kb - 1, then this): bit-identical
+  apply_pending(st);
   f4_t dblk[RG][NMAT][NTT];
 #pragma unroll
   for (int piece = 0; piece < 2; piece++) {
@@ -319,10 +341,9 @@ __device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
       for (int t = 0; t < NTT; t++) {
         st.acc[rg][m][t] =
             __builtin_amdgcn_mfma_f32_16x16x32_f16(sv[t], mo, st.acc[rg][m][t], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          st.acc[rg][m][t][i] = __builtin_fmaf(d, dblk[rg][m][t][i], st.acc[rg][m][t][i]);
+        st.pend[rg][m][t] = dblk[rg][m][t];
       }
+      st.pend_d[rg][m] = d;
     }
 }
 
@@ -406,7 +427,11 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-      for (int t = 0; t < NTT; t++) st.acc[rg][m][t] = zero4;
+      for (int t = 0; t < NTT; t++) st.acc[rg][m][t] = st.pend[rg][m][t] = zero4;
+#pragma unroll
+  for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) st.pend_d[rg][m] = 0.0f;
 
   // prologue: weights of column 0, activations of column 0, weights of
   // columns 1 .. A_AHEAD - 1
@@ -415,6 +440,7 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
 #pragma unroll
   for (int c = 1; c < A_AHEAD; c++) issue_a(st, c < NKB ? c : NKB - 1);
   for (int kb = 0; kb < NKB; kb++) mfma_step(st, kb);
+  apply_pending(st);  // the last column's d * Dblk
   // drain the trailing re-copies before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
