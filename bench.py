@@ -124,13 +124,14 @@ def stage_bytes(stage, U, T, K, decode, shared_q8=False):
     return 0
 
 
-def dominant_kernel(stage, T, path):
-    """Kernel name of a stage on the path the library picks for T tokens."""
-    if T == 1 and path == 0:
+def dominant_kernel(stage, last_path):
+    """Kernel name of a stage on the path the last forward ran
+    (hy3x_layer_last_path)."""
+    if last_path == 0:
         return {"gateup": "k_gateup_decode", "down": "k_down_decode"}[stage]
-    mfma = path >= 2 or (path == 0 and T >= 2)
-    if mfma:
-        return {"gateup": "k_moe_mfma<true>", "down": "k_moe_mfma<false>"}[stage]
+    if last_path in (3, 4):
+        ns = "mfma_wide" if last_path == 4 else "mfma_narrow"
+        return {"gateup": f"{ns}::k_moe_mfma<true>", "down": f"{ns}::k_moe_mfma<false>"}[stage]
     return {"gateup": "k_gateup_gemv<4>", "down": "k_down_gemv<4>"}[stage]
 
 
@@ -204,7 +205,7 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
         L.set_timing(False)
     stage_us = {k: v * 1e3 / max(nfw, 1) for k, v in stages.items()}
     dom = max(("gateup", "down"), key=lambda k: stage_us[k])
-    kernel = dominant_kernel(dom, cfg.T, layers[0].path)
+    kernel = dominant_kernel(dom, layers[0].last_path())
     decode = cfg.T == 1 and layers[0].path == 0
     dom_bytes = stage_bytes(dom, U, cfg.T, cfg.K, decode, shared_q8)
     # launch duration of the dominant kernel: replayed back to back on the launch

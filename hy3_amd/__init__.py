@@ -60,6 +60,7 @@ _SIGS = {
     "hy3x_layer_forward_residual": (I32, [P, P, P, I32, I32, F32, P]),
     "hy3x_layer_last_routing": (I32, [P, P, P, P]),
     "hy3x_layer_set_path": (I32, [P, I32]),
+    "hy3x_layer_last_path": (I32, [P, ctypes.POINTER(ctypes.c_int)]),
     "hy3x_layer_time_stage": (I32, [P, I32, I32, P, ctypes.POINTER(ctypes.c_float)]),
     "hy3x_diag_read_rate": (I32, [P, I64, I64, I32, P, ctypes.POINTER(ctypes.c_float)]),
     "hy3x_layer_set_timing": (I32, [P, I32]),
@@ -211,6 +212,13 @@ class MoELayer:
     def set_path(self, path):
         _check(lib().hy3x_layer_set_path(self._h, path))
         self.path = path
+
+    def last_path(self):
+        """Expert path of the last forward: 0 decode kernels, 1 GEMV tiles,
+        3 / 4 MFMA narrow / wide tiles."""
+        v = ctypes.c_int()
+        _check(lib().hy3x_layer_last_path(self._h, ctypes.byref(v)))
+        return v.value
 
     STAGES = ("router", "dispatch", "gateup", "down", "combine")
 

@@ -300,6 +300,14 @@ int hy3x_layer_set_path(hy3x_layer *L, int path) {
   return HY3X_OK;
 }
 
+int hy3x_layer_last_path(const hy3x_layer *L, int *path) {
+  if (!L || !path) return fail(HY3X_E_ARG, "NULL argument");
+  if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
+  const auto &c = L->cur;
+  *path = c.mode == Mode::DECODE ? 0 : c.mode == Mode::GEMV ? 1 : c.wide ? 4 : 3;
+  return HY3X_OK;
+}
+
 // Kernels of one stage for the forward described by L->cur (shared by the
 // forward and the kernel replay used for timing).
 static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {

@@ -194,6 +194,12 @@ int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
  * the wide tile shape (64 tokens). */
 int hy3x_layer_set_path(hy3x_layer *layer, int path);
 
+/* Which expert path the last forward ran: 0 = the fused single-token decode
+ * kernels, 1 = wavefront-GEMV tiles, 3 = MFMA with the narrow tile shape,
+ * 4 = MFMA with the wide one (diagnostics and benchmarks: the kernel whose
+ * roofline a benchmark reports). */
+int hy3x_layer_last_path(const hy3x_layer *layer, int *path);
+
 /* ---- synthetic inputs (test / benchmark data, not part of the MoE path) ----
  * Device-side generator + Q4_K quantiser for the seeded synthetic layers the
  * benchmark configurations describe. The quantiser reproduces hy3_convert.c's

@@ -281,18 +281,23 @@ def test_routing_with_ties(torch, T, case):
     assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [1, 7, 64, 200])
+@pytest.mark.parametrize("T", [1, 7, 64, 200, 400])
 def test_expert_paths_match_oracle(torch, layer, cpu, T):
     """Every expert path (0 automatic, 1 wavefront GEMV, 2 MFMA grouped GEMM,
     3 / 4 its narrow / wide tile shape) meets the tolerance on the same
-    tokens; routing is identical on all."""
+    tokens; routing is identical on all; hy3x_layer_last_path reports the
+    path that ran (automatic: decode kernels at T = 1, the narrow MFMA shape
+    below 384 tokens, the wide one from there)."""
     x = C.inputs(0xC2, T, first_token=300)
     rows = np.linspace(0, T - 1, min(T, 6)).astype(int)
     yo, ro = cpu.forward(x[rows])
+    mfma_auto = 4 if T >= 384 else 3
+    ran = {0: 0 if T == 1 else mfma_auto, 1: 1, 2: mfma_auto, 3: 3, 4: 4}
     try:
         for path in (0, 1, 2, 3, 4):
             layer.set_path(path)
             y, ids, _, _ = run(torch, layer, x)
+            assert layer.last_path() == ran[path], path
             assert np.array_equal(ids[rows], ro["ids"]), path
             assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL, path
     finally:
