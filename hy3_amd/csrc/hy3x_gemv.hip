@@ -155,12 +155,12 @@ __global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ w
 // Decode fast path (T = 1): no dispatch. Slot k < K is routed expert ids[k],
 // slot K the shared expert; the expert id is one load away from the weights.
 
-// Routed gate/up of a single token: block = 16 rows (four waves x 4) of
-// routed slot blockIdx.x / 96. Every block routes the token itself from the
-// 192 sigmoid values / scores (the routing contract, identical in every
-// block: topk_block) and takes expert sids[slot]; block 0 publishes the
-// routing and the stats. 768 blocks at 3 per CU: all resident at once.
-__global__ __launch_bounds__(256) void k_gateup_decode(
+// Routed gate/up of a single token: block = DEC_GU_RPB rows (DEC_GU_WAVES
+// waves x 4) of routed slot blockIdx.x / DEC_GU_BLOCKS. Every block routes the
+// token itself from the 192 sigmoid values / scores (the routing contract,
+// identical in every block: topk_block) and takes expert sids[slot]; block 0
+// publishes the routing and the stats. All blocks are resident at once.
+__global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ s16,
     const float *__restrict__ sig, const float *__restrict__ score, int K, float scale,
     int32_t *__restrict__ ids, float *__restrict__ wpre, float *__restrict__ wout,
@@ -172,14 +172,20 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
   // the token's staged s, once per block (the four waves read it from LDS),
   // loaded together with the routing inputs
   const int tid = threadIdx.x;
-  const uint4 sa = reinterpret_cast<const uint4 *>(s16)[tid];
-  const uint4 sb = reinterpret_cast<const uint4 *>(s16)[tid + 256];
+  constexpr int NT = 64 * DEC_GU_WAVES, NS = (D / 8 + NT - 1) / NT;  // 16-byte pieces per thread
+  constexpr bool EXACT = NS * NT == D / 8;
+  uint4 sv[NS];
+#pragma unroll
+  for (int i = 0; i < NS; i++)
+    sv[i] = EXACT || tid + NT * i < D / 8 ? reinterpret_cast<const uint4 *>(s16)[tid + NT * i]
+                                          : make_uint4(0u, 0u, 0u, 0u);
   __shared__ __attribute__((aligned(16))) __half s_l[D];
   __shared__ int32_t sids[KMAX], scratch_l[4 * E + 2 * KMAX + 2];
   __shared__ float swp[KMAX], sw[KMAX], sg_l[E];
-  reinterpret_cast<uint4 *>(s_l)[tid] = sa;
-  reinterpret_cast<uint4 *>(s_l)[tid + 256] = sb;
-  // s_l is visible after topk_block's first barrier; waves 1-3 unpack their
+#pragma unroll
+  for (int i = 0; i < NS; i++)
+    if (EXACT || tid + NT * i < D / 8) reinterpret_cast<uint4 *>(s_l)[tid + NT * i] = sv[i];
+  // s_l is visible after topk_block's first barrier; the other waves unpack their
   // s groups while wave 0 finishes the routing
   topk_block<false>(sig, score, K, scale, sids, swp, sw, sg_l, scratch_l, trace);
   uint32_t X[32];
@@ -200,7 +206,8 @@ __global__ __launch_bounds__(256) void k_gateup_decode(
       stats[1] += (unsigned long long)(K + 1);
     }
   }
-  gateup_rows<DEC_RPW, DEC_GU_PF>(wq, e, slot, rc * DEC_RPB + wave * DEC_RPW, X, slo, shi, h16);
+  gateup_rows<DEC_RPW, DEC_GU_PF>(wq, e, slot, rc * DEC_GU_RPB + wave * DEC_RPW, X, slo, shi,
+                                  h16);
   trace_point(trace, 3);
 }
 

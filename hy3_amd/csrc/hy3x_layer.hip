@@ -317,7 +317,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
   switch (stage) {
     case HY3X_STAGE_ROUTER:
       if (c.mode == Mode::DECODE) {
-        k_route_decode<<<E + DEC_GU_BLOCKS, 256, 0, st>>>(
+        k_route_decode<<<E + DEC_SH_BLOCKS, 256, 0, st>>>(
             x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
             L->s16, L->s32, L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16, L->trace[0]);
         break;
@@ -360,7 +360,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_GATEUP:
       if (c.mode == Mode::DECODE)
-        k_gateup_decode<<<K * DEC_GU_BLOCKS, 256, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
+        k_gateup_decode<<<K * DEC_GU_BLOCKS, 64 * DEC_GU_WAVES, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
                                                           c.scale, L->ids, L->wpre, L->w,
                                                           L->stats, L->h16, L->trace[1]);
       else if (c.mode == Mode::MFMA && c.wide)

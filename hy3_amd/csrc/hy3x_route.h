@@ -182,7 +182,8 @@ __device__ __forceinline__ void topk_block(const float *sig, const float *score,
 #pragma unroll
   for (int m = 0; m < 3; m++) v[m] = score[lane + 64 * m];
   float4 q4[12];
-  const float4 *qsrc = reinterpret_cast<const float4 *>(score + 48 * wave);
+  // waves past the fourth (wider blocks) repeat a quarter and keep no count
+  const float4 *qsrc = reinterpret_cast<const float4 *>(score + 48 * (wave & 3));
 #pragma unroll
   for (int u = 0; u < 12; u++) q4[u] = qsrc[u];
   const float sgv = tid < E ? sig[tid] : 0.0f;
@@ -200,7 +201,8 @@ __device__ __forceinline__ void topk_block(const float *sig, const float *score,
       cnt[m] += (int)(qx > v[m]) + (int)(qy > v[m]) + (int)(qz > v[m]) + (int)(qw > v[m]);
   }
 #pragma unroll
-  for (int m = 0; m < 3; m++) part_l[wave * E + lane + 64 * m] = cnt[m];
+  for (int m = 0; m < 3; m++)
+    if (wave < 4) part_l[wave * E + lane + 64 * m] = cnt[m];
   if (tid < E) sg_l[tid] = sgv;
   __syncthreads();
   if (trace) trace_point(trace, 4);
