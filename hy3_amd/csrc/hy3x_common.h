@@ -124,6 +124,17 @@ __device__ __forceinline__ void trace_point(unsigned long long *trace_buf, int i
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
+// The staged fp16 h = silu(g) * u: the product rounded to fp32, then to fp16.
+// The empty asm pins the fp32 product in a register: otherwise the backend
+// fuses the multiply into the conversion (v_fma_mix, one rounding) for some
+// accumulator elements and not others, and a token's h then depends on its
+// row in the MFMA tile. Every kernel and element now rounds the same way.
+__device__ __forceinline__ __half swiglu_h(float g, float u) {
+  float h = silu(g) * u;
+  asm volatile("" : "+v"(h));
+  return __float2half(h);
+}
+
 // Four elements of the residual stream x, plus the addend xadd when the
 // forward carries one (x + attn_out, the residual add of hy3.c:1264 and of
 // add_rmsnorm_kernel, hy3_gpu.cu:453-460; the same fp32 add in every reader).

@@ -53,7 +53,7 @@ struct GateupRows {
       unpack_group(cur[4], cur[5], P);
       const float uv = group_dot(P, X, slo, shi, block_scale(cur[3], sel));
       const float g = wave_total(gv), u = wave_total(uv);
-      if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
+      if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = swiglu_h(g, u);
     }
   }
 };

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void k_gateup_gemv(const uint8_t *__restrict__
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
       const float g = wave_total(gv[tt]), u = wave_total(uv[tt]);
-      if (lane == 0 && tt < n) h16[(size_t)slot[tt] * F + stage_index(r)] = __float2half(silu(g) * u);
+      if (lane == 0 && tt < n) h16[(size_t)slot[tt] * F + stage_index(r)] = swiglu_h(g, u);
     }
   }
 }

@@ -367,7 +367,7 @@ __device__ __forceinline__ void store_tile(
           const int slot = t_slot[tok];
           if constexpr (GATEUP) {
             h16m[(size_t)slot * F + perm8(r)] =
-                __float2half(silu(acc[rg][0][t][i]) * acc[rg][1][t][i]);
+                swiglu_h(acc[rg][0][t][i], acc[rg][1][t][i]);
           } else {
             out[(size_t)slot * D + r] = acc[rg][0][t][i];
           }

@@ -111,7 +111,7 @@ struct GateupRowsQ8 {
       if (rr + PF < RPW) issue(rr + PF, ring[rr % PF]);
       const float g = wave_total(q8_group_dot(cur[0], X, slo, shi));
       const float u = wave_total(q8_group_dot(cur[1], X, slo, shi));
-      if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = __float2half(silu(g) * u);
+      if (lane == 0) h16[(size_t)slot * F + stage_index(r0 + rr)] = swiglu_h(g, u);
     }
   }
 };
