@@ -260,6 +260,19 @@ def test_token_permutation_full_size(torch, layer, cpu):
     assert np.array_equal(yp.view(np.uint32), y[perm].view(np.uint32))
 
 
+def test_batch_invariance(torch, layer):
+    """For T >= 2 a token's output does not depend on the other tokens of
+    its forward: three tokens alone, inside a batch of 40 (narrow tiles) and
+    inside a batch of 500 (wide tiles) give the same bits."""
+    x = C.inputs(0xC8, 500)
+    pick = np.array([3, 17, 33])
+    alone, *_ = run(torch, layer, x[pick])
+    mid, *_ = run(torch, layer, x[:40])
+    big, *_ = run(torch, layer, x)
+    assert np.array_equal(alone.view(np.uint32), mid[pick].view(np.uint32))
+    assert np.array_equal(alone.view(np.uint32), big[pick].view(np.uint32))
+
+
 def test_deterministic(torch, layer):
     x = C.inputs(0xC2, 64)
     y1, *_ = run(torch, layer, x)
