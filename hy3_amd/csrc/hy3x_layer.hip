@@ -334,16 +334,16 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : L->s16, L->s32,
                                      mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt);
         if (T <= kTinyRouterT)
-          k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
+          k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else if (T <= kMidRouterT)
-          k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
+          k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else if (T <= kLargeRouterT)
-          k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE><<<dim3((T + 15) / 16, E / 32), 256, 0, st>>>(
+          k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 15) / 16, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else
-          k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
+          k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
       }
       k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, T, L->ids,

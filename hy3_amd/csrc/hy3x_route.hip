@@ -269,12 +269,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
 // k-major in LDS (double-buffered, next chunk prefetched into registers). The
 // chunk is large (few blocks run at small T, so each K step's load latency is
 // paid in sequence: the fewer steps, the better).
-template <int MT, int ME, int TG, int EG, int KC>
+template <int MT, int ME, int TG, int EG, int KC, int R>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s32,
                                                      const float *__restrict__ router, int T,
                                                      float *__restrict__ logits) {
   static_assert(8 * TG * EG == 256, "256 threads");
   static_assert(D % KC == 0 && KC % 8 == 0, "K chunks");
+  constexpr int NCH = D / KC;
+  static_assert(R >= 1 && NCH % R == 0, "whole rounds of the fetch ring");
   constexpr int TT = MT * TG, TE = ME * EG;
   constexpr int SP = TT + 4, WP = TE + 4;        // padded LDS rows (floats)
   constexpr int NS = TT * KC / 4 / 256, NW = TE * KC / 4 / 256;  // float4 per thread
@@ -282,36 +284,41 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
   __shared__ float sl[2][KC][SP], wl[2][KC][WP];
   const int t0 = blockIdx.x * TT, e0 = blockIdx.y * TE;
   const int tid = threadIdx.x, v = tid & 7, mt = tid >> 3, tg = mt % TG, eg = mt / TG;
-  float4 sn[NS], wn[NW];
-  auto fetch = [&](int k0) {
+  // a register ring of R chunks in flight (the loop is unrolled by R so that
+  // the ring slots stay static)
+  float4 sn[R][NS], wn[R][NW];
+  // Loads are unconditional (rows past T read row T - 1 and are zeroed when
+  // staged; fetches past the end re-read the last chunk), so that the wait
+  // counters stay exact through the ring and no fetch waits on a later one.
+  auto fetch = [&](int k0, float4(&sd)[NS], float4(&wd)[NW]) {
 #pragma unroll
     for (int u = 0; u < NS; u++) {
       const int q = tid + 256 * u, r = q % TT, c = q / TT, tt = t0 + r;
-      sn[u] = tt < T ? reinterpret_cast<const float4 *>(s32 + (size_t)tt * D + k0)[c]
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      sd[u] = reinterpret_cast<const float4 *>(s32 + (size_t)(tt < T ? tt : T - 1) * D + k0)[c];
     }
 #pragma unroll
     for (int u = 0; u < NW; u++) {
       const int q = tid + 256 * u, r = q % TE, c = q / TE;
-      wn[u] = reinterpret_cast<const float4 *>(router + (size_t)(e0 + r) * D + k0)[c];
+      wd[u] = reinterpret_cast<const float4 *>(router + (size_t)(e0 + r) * D + k0)[c];
     }
   };
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, const float4(&sd)[NS], const float4(&wd)[NW]) {
 #pragma unroll
     for (int u = 0; u < NS; u++) {  // neighbouring lanes write neighbouring words
       const int q = tid + 256 * u, r = q % TT, c = q / TT;
-      sl[buf][4 * c + 0][r] = sn[u].x;
-      sl[buf][4 * c + 1][r] = sn[u].y;
-      sl[buf][4 * c + 2][r] = sn[u].z;
-      sl[buf][4 * c + 3][r] = sn[u].w;
+      const bool in = t0 + r < T;
+      sl[buf][4 * c + 0][r] = in ? sd[u].x : 0.0f;
+      sl[buf][4 * c + 1][r] = in ? sd[u].y : 0.0f;
+      sl[buf][4 * c + 2][r] = in ? sd[u].z : 0.0f;
+      sl[buf][4 * c + 3][r] = in ? sd[u].w : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < NW; u++) {
       const int q = tid + 256 * u, r = q % TE, c = q / TE;
-      wl[buf][4 * c + 0][r] = wn[u].x;
-      wl[buf][4 * c + 1][r] = wn[u].y;
-      wl[buf][4 * c + 2][r] = wn[u].z;
-      wl[buf][4 * c + 3][r] = wn[u].w;
+      wl[buf][4 * c + 0][r] = wd[u].x;
+      wl[buf][4 * c + 1][r] = wd[u].y;
+      wl[buf][4 * c + 2][r] = wd[u].z;
+      wl[buf][4 * c + 3][r] = wd[u].w;
     }
   };
   float acc[MT][ME];
@@ -319,24 +326,28 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
   for (int a = 0; a < MT; a++)
 #pragma unroll
     for (int b = 0; b < ME; b++) acc[a][b] = 0.0f;
-  fetch(0);
-  for (int k0 = 0, it = 0; k0 < D; k0 += KC, it++) {
-    const int buf = it & 1;
-    stage(buf);
-    __syncthreads();  // buf staged; the other buffer is no longer read
-    if (k0 + KC < D) fetch(k0 + KC);
+#pragma unroll
+  for (int r = 0; r < R; r++) fetch(r * KC, sn[r], wn[r]);
+  for (int it0 = 0; it0 < NCH; it0 += R) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int it = it0 + r, buf = it & 1;
+      stage(buf, sn[r], wn[r]);
+      __syncthreads();  // buf staged; the other buffer is no longer read
+      fetch((it + R < NCH ? it + R : NCH - 1) * KC, sn[r], wn[r]);
 #pragma unroll 4
-    for (int ii = 0; ii < KC / 8; ii++) {
-      const int k = 8 * ii + v;
-      float sv[MT], wv[ME];
+      for (int ii = 0; ii < KC / 8; ii++) {
+        const int k = 8 * ii + v;
+        float sv[MT], wv[ME];
 #pragma unroll
-      for (int a = 0; a < MT; a++) sv[a] = sl[buf][k][MT * tg + a];
+        for (int a = 0; a < MT; a++) sv[a] = sl[buf][k][MT * tg + a];
 #pragma unroll
-      for (int b = 0; b < ME; b++) wv[b] = wl[buf][k][ME * eg + b];
+        for (int b = 0; b < ME; b++) wv[b] = wl[buf][k][ME * eg + b];
 #pragma unroll
-      for (int a = 0; a < MT; a++)
+        for (int a = 0; a < MT; a++)
 #pragma unroll
-        for (int b = 0; b < ME; b++) acc[a][b] = __builtin_fmaf(wv[b], sv[a], acc[a][b]);
+          for (int b = 0; b < ME; b++) acc[a][b] = __builtin_fmaf(wv[b], sv[a], acc[a][b]);
+      }
     }
   }
 #pragma unroll
@@ -348,14 +359,14 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
       if (v == 0 && tt < T) logits[(size_t)tt * E + ee] = lg;
     }
 }
-template __global__ void k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE>(const float *, const float *,
-                                                                    int, float *);
-template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE>(const float *, const float *,
-                                                                    int, float *);
-template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID>(const float *, const float *,
-                                                                  int, float *);
-template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID>(const float *, const float *,
-                                                                  int, float *);
+template __global__ void k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
+    const float *, const float *, int, float *);
+template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
+    const float *, const float *, int, float *);
+template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
+    const float *, const float *, int, float *);
+template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY>(
+    const float *, const float *, int, float *);
 
 // Routing of one token per block (T > 1 paths): sigmoid and scores of the
 // 192 logits, then the top-K.
