@@ -78,40 +78,39 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
   constexpr int G = F / 64;
   const int lane = threadIdx.x & 63, hw = lane >> 5, gl = lane & 31;
   const bool active = gl < G;
-  const int b = gl >> 2, p = gl & 3;
+  // Every lane loads (the 8 idle lanes of each half re-read group G - 1 and
+  // drop it): loads under a lane condition make the compiler wait for the
+  // whole ring at every pass, which serialises the passes.
+  const int glc = active ? gl : G - 1;
+  const int b = glc >> 2, p = glc & 3;
   const ScaleSel sel(p);
   const uint8_t *dbase = wq + (size_t)e * EXPERT_BYTES + 2 * MAT_BYTES + (size_t)b * QB;
   uint4 ring[PF][3];
   auto issue = [&](int ps, uint4 (&dst)[3]) {
-    if (active) {
-      const uint8_t *dp = dbase + (size_t)(r0 + 2 * ps + hw) * (F / QK) * QB;
-      dst[0] = *reinterpret_cast<const uint4 *>(dp);
-      dst[1] = *reinterpret_cast<const uint4 *>(dp + 16 + 32 * p);
-      dst[2] = *reinterpret_cast<const uint4 *>(dp + 32 + 32 * p);
-    }
+    const uint8_t *dp = dbase + (size_t)(r0 + 2 * ps + hw) * (F / QK) * QB;
+    dst[0] = *reinterpret_cast<const uint4 *>(dp);
+    dst[1] = *reinterpret_cast<const uint4 *>(dp + 16 + 32 * p);
+    dst[2] = *reinterpret_cast<const uint4 *>(dp + 32 + 32 * p);
   };
   // h first: loads complete in issue order for the wait counters, so h
   // issued after the weight ring would hold the first pass back until the
   // whole ring had landed
   uint32_t X[32];
-  if (active) load_group_x(h, gl, X);
+  load_group_x(h, glc, X);
 #pragma unroll
   for (int ps = 0; ps < PF && ps < PASSES; ps++) issue(ps, ring[ps]);
   float slo = 0.0f, shi = 0.0f;
-  if (active) group_sums(X, slo, shi);
+  group_sums(X, slo, shi);
 #pragma unroll
   for (int ps = 0; ps < PASSES; ps++) {
     uint4 cur[3];
 #pragma unroll
     for (int q = 0; q < 3; q++) cur[q] = ring[ps % PF][q];
     if (ps + PF < PASSES) issue(ps + PF, ring[ps % PF]);
-    float dv = 0.0f;
-    if (active) {
-      uint32_t P[32];
-      unpack_group(cur[1], cur[2], P);
-      dv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
-    }
-    fn(ps, half_totals(dv));
+    uint32_t P[32];
+    unpack_group(cur[1], cur[2], P);
+    const float dv = group_dot(P, X, slo, shi, block_scale(cur[0], sel));
+    fn(ps, half_totals(active ? dv : 0.0f));
   }
 }
 

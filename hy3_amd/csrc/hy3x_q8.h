@@ -134,23 +134,24 @@ __device__ __forceinline__ void down_rows_q8(const uint8_t *__restrict__ wsh,
   constexpr int G = F / 64, ROWB = F / Q8K * QB;  // 24 groups, 1728 bytes per down row
   const int lane = threadIdx.x & 63, hw = lane >> 5, gl = lane & 31;
   const bool active = gl < G;
+  const int glc = active ? gl : G - 1;  // unconditional loads, as down_rows
   const uint8_t *dbase = wsh + 2 * Q8_MAT_BYTES;
   uint32_t X[32];
-  if (active) load_group_x(h, gl, X);  // h first: loads complete in issue order
+  load_group_x(h, glc, X);  // h first: loads complete in issue order
   Q8Group ring[PF];
   auto issue = [&](int ps, Q8Group &dst) {
-    if (active) load_q8_group(dbase + (size_t)(r0 + 2 * ps + hw) * ROWB, gl, dst);
+    load_q8_group(dbase + (size_t)(r0 + 2 * ps + hw) * ROWB, glc, dst);
   };
 #pragma unroll
   for (int ps = 0; ps < PF && ps < PASSES; ps++) issue(ps, ring[ps]);
   float slo = 0.0f, shi = 0.0f;
-  if (active) group_sums(X, slo, shi);
+  group_sums(X, slo, shi);
 #pragma unroll
   for (int ps = 0; ps < PASSES; ps++) {
     const Q8Group cur = ring[ps % PF];
     if (ps + PF < PASSES) issue(ps + PF, ring[ps % PF]);
-    const float dv = active ? q8_group_dot(cur, X, slo, shi) : 0.0f;
-    fn(ps, half_totals(dv));
+    const float dv = q8_group_dot(cur, X, slo, shi);
+    fn(ps, half_totals(active ? dv : 0.0f));
   }
 }
 
