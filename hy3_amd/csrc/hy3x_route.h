@@ -186,7 +186,9 @@ __device__ __forceinline__ void topk_block(const float *sig, const float *score,
   const float4 *qsrc = reinterpret_cast<const float4 *>(score + 48 * (wave & 3));
 #pragma unroll
   for (int u = 0; u < 12; u++) q4[u] = qsrc[u];
-  const float sgv = tid < E ? sig[tid] : 0.0f;
+  // unconditional (a clamped index): a load under a lane condition would wait
+  // for the loads issued before it
+  const float sgv = sig[tid < E ? tid : E - 1];
   if (tid < KMAX) cnt_l[tid] = 0;
   if (tid == 0) *flag_l = 0;
   int cnt[3] = {0, 0, 0};
