@@ -69,6 +69,7 @@ def parse():
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
 
 def measured_traffic(workload, kernel):
@@ -213,6 +214,12 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
     reps = max(10, min(steps, 2000))
     launch_us = layers[-1].time_stage(dom, reps, stream=stream)
     achieved = dom_bytes / (launch_us * 1e-6) / 1e9
+    # the kernel's binding roofline: its arithmetic intensity against the
+    # machine balance (2.5 PFLOP/s dense fp16 MFMA over 8 TB/s = 312 flop/B)
+    per_slot = (4 if dom == "gateup" else 2) * 1536 * 4096  # flop per (token, expert)
+    dom_flops = 0 if decode else per_slot * cfg.T * (cfg.K + 1)
+    tflops = dom_flops / (launch_us * 1e-6) / 1e12
+    mfma_bound = dom_flops / dom_bytes > PEAK_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
     alg_bytes = (C.algorithmic_bytes(cfg.T, U) + (3 * (Q8MAT - MAT) if shared_q8 else 0)) * cfg.n_layers
     flops = C.algorithmic_flops(cfg.T, cfg.K) * cfg.n_layers
     for L in layers:
@@ -220,11 +227,19 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
     return dict(
         tokens_per_s=tokens_per_s, ms_per_step=ms, U=U, layer_GBps=alg_bytes / (ms * 1e-3) / 1e9,
         layer_TFLOPs=flops / (ms * 1e-3) / 1e12, stage_us=stage_us,
-        roofline=dict(bound="hbm", kernel=kernel, achieved=round(achieved, 1), peak=PEAK_HBM_GBS,
-                      unit="GB/s", frac=round(achieved / PEAK_HBM_GBS, 4),
-                      traffic=measured_traffic(f"config{cfg.index}:{cfg.name}", kernel),
-                      bytes_per_launch=int(dom_bytes), launch_us=round(launch_us, 3),
-                      launch_timing=f"HIP events around {reps} back-to-back launches"),
+        roofline=(dict(bound="mfma", kernel=kernel, achieved=round(tflops, 1),
+                       peak=PEAK_MFMA_TFLOPS, unit="TFLOP/s",
+                       frac=round(tflops / PEAK_MFMA_TFLOPS, 4),
+                       hbm_GBps=round(achieved, 1), hbm_frac=round(achieved / PEAK_HBM_GBS, 4))
+                  if mfma_bound else
+                  dict(bound="hbm", kernel=kernel, achieved=round(achieved, 1), peak=PEAK_HBM_GBS,
+                       unit="GB/s", frac=round(achieved / PEAK_HBM_GBS, 4),
+                       **({} if decode else dict(mfma_TFLOPs=round(tflops, 1),
+                                                 mfma_frac=round(tflops / PEAK_MFMA_TFLOPS, 4)))))
+        | dict(traffic=measured_traffic(f"config{cfg.index}:{cfg.name}", kernel),
+               bytes_per_launch=int(dom_bytes), flops_per_launch=int(dom_flops),
+               launch_us=round(launch_us, 3),
+               launch_timing=f"HIP events around {reps} back-to-back launches"),
     )
 
 
