@@ -156,10 +156,11 @@ __global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ w
 // slot K the shared expert; the expert id is one load away from the weights.
 
 // Routed gate/up of a single token: block = DEC_GU_RPB rows (DEC_GU_WAVES
-// waves x 4) of routed slot blockIdx.x / DEC_GU_BLOCKS. Every block routes the
+// waves x 4) of routed slot blockIdx.x / DEC_GU_BLOCKS. Every wave routes the
 // token itself from the 192 sigmoid values / scores (the routing contract,
-// identical in every block: topk_block) and takes expert sids[slot]; block 0
-// publishes the routing and the stats. All blocks are resident at once.
+// identical in every wave and block: topk_wave_fast, or topk_wave_regs on a
+// tie) and takes the expert of its slot; block 0 publishes the routing and
+// the stats. All blocks are resident at once.
 __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ s16,
     const float *__restrict__ sig, const float *__restrict__ score, int K, float scale,
@@ -179,32 +180,53 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
   for (int i = 0; i < NS; i++)
     sv[i] = EXACT || tid + NT * i < D / 8 ? reinterpret_cast<const uint4 *>(s16)[tid + NT * i]
                                           : make_uint4(0u, 0u, 0u, 0u);
+  // the routing inputs: expert lane + 64 m's score and sigma
+  float sc[3], sg[3];
+#pragma unroll
+  for (int m = 0; m < 3; m++) {
+    sc[m] = score[lane + 64 * m];
+    sg[m] = sig[lane + 64 * m];
+  }
   __shared__ __attribute__((aligned(16))) __half s_l[D];
-  __shared__ int32_t sids[KMAX], scratch_l[4 * E + 2 * KMAX + 2];
-  __shared__ float swp[KMAX], sw[KMAX], sg_l[E];
+  __shared__ int32_t sids[KMAX];
+  __shared__ float swp[KMAX], sw[KMAX];
 #pragma unroll
   for (int i = 0; i < NS; i++)
     if (EXACT || tid + NT * i < D / 8) reinterpret_cast<uint4 *>(s_l)[tid + NT * i] = sv[i];
-  // s_l is visible after topk_block's first barrier; the other waves unpack their
-  // s groups while wave 0 finishes the routing
-  topk_block<false>(sig, score, K, scale, sids, swp, sw, sg_l, scratch_l, trace);
-  uint32_t X[32];
-  load_group_x(s_l, lane, X);
-  float slo, shi;
-  group_sums(X, slo, shi);
-  __syncthreads();
-  trace_point(trace, 1);
-  const int e = sids[slot];
-  if (blockIdx.x == 0) {
-    if (threadIdx.x < K) {
+  // every wave routes the token itself, in registers (the same arithmetic in
+  // every wave and block, so the outcome is block-uniform)
+  int my_e;
+  float my_sig, sum;
+  const bool fast = topk_wave_fast(sc, sg, K, my_e, my_sig, sum);
+  __syncthreads();  // s_l staged
+  int e;
+  if (fast) {
+    e = __builtin_amdgcn_readlane(my_e, slot);
+    if (blockIdx.x == 0 && threadIdx.x < K) {
+      const float inv = 1.0f / (sum + 1e-20f);
+      const float v = my_sig * inv;
+      ids[threadIdx.x] = my_e;
+      wpre[threadIdx.x] = v;
+      wout[threadIdx.x] = v * scale;
+    }
+  } else {  // a tie or a NaN among the scores: the reference's selection with swaps
+    if (wave == 0) topk_wave_regs(sc, sg, K, scale, sids, swp, sw);
+    __syncthreads();
+    e = sids[slot];
+    if (blockIdx.x == 0 && threadIdx.x < K) {
       ids[threadIdx.x] = sids[threadIdx.x];
       wpre[threadIdx.x] = swp[threadIdx.x];
       wout[threadIdx.x] = sw[threadIdx.x];
     }
-    if (threadIdx.x == 0 && stats) {  // forwards, experts touched (shared included)
-      stats[0] += 1ull;
-      stats[1] += (unsigned long long)(K + 1);
-    }
+  }
+  uint32_t X[32];
+  load_group_x(s_l, lane, X);
+  float slo, shi;
+  group_sums(X, slo, shi);
+  trace_point(trace, 1);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && stats) {  // forwards, experts touched (shared included)
+    stats[0] += 1ull;
+    stats[1] += (unsigned long long)(K + 1);
   }
   gateup_rows<DEC_RPW, DEC_GU_PF>(wq, e, slot, rc * DEC_GU_RPB + wave * DEC_RPW, X, slo, shi,
                                   h16);

@@ -346,8 +346,14 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
           k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
       }
-      k_topk<<<T, 256, 0, st>>>(L->logits, L->bias, L->has_bias, K, c.scale, T, L->ids,
-                                L->wpre, L->w, L->bits, L->wt);
+      {
+        // one wave per token; up to 256 tokens one wave per block, so that
+        // few tokens still spread over many CUs
+        const int wpb = T <= 256 ? 1 : 4;
+        k_topk<<<(T + wpb - 1) / wpb, 64 * wpb, 0, st>>>(L->logits, L->bias, L->has_bias, K,
+                                                         c.scale, T, L->ids, L->wpre, L->w,
+                                                         L->bits, L->wt);
+      }
       break;
     case HY3X_STAGE_DISPATCH:
       if (c.mode == Mode::MFMA && T <= kSmallRouterT)

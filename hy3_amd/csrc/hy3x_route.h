@@ -60,6 +60,17 @@ __device__ __forceinline__ float tree8_lanes(float c, int v) {
   return __shfl(res, (threadIdx.x & 63) & ~7, 64);
 }
 
+// Element m (wave-uniform) of lane l's three-value array, as a wave-uniform
+// value. Each of the three is read out of lane l first and the choice is made
+// between the scalars: a select between the array elements themselves can be
+// lowered to an indexed copy through scratch memory.
+__device__ __forceinline__ float pick3_lane(const float (&a)[3], int m, int l) {
+  const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[0]), l));
+  const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[1]), l));
+  const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[2]), l));
+  return m == 0 ? a0 : (m == 1 ? a1 : a2);
+}
+
 // Best candidate of the wave: largest score, ties to the lowest current
 // position (key = position * 256 + expert). Every lane returns the winner.
 __device__ __forceinline__ void wave_best(float &v, int &key) {
@@ -121,10 +132,7 @@ __device__ __forceinline__ void topk_wave_regs(const float (&sc)[3], const float
       if (pos[m] == k) pos[m] = bp;               // the element at position k moves
       if (lane + 64 * m == be) pos[m] = k;        // the winner takes position k
     }
-    const int bm = be >> 6;
-    const float sv = bm == 0 ? sg[0] : (bm == 1 ? sg[1] : sg[2]);
-    const float s_be =
-        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), be & 63));
+    const float s_be = pick3_lane(sg, be >> 6, be & 63);
     sum = sum + s_be;
     if (lane == k) {
       my_e = be;
@@ -140,104 +148,61 @@ __device__ __forceinline__ void topk_wave_regs(const float (&sc)[3], const float
   }
 }
 
-// The same from 192-entry arrays sig / score (global or LDS).
-__device__ __forceinline__ void topk_wave(const float *sig, const float *score, int K, float scale,
-                                          int32_t *ids, float *wpre, float *wout) {
+// Top-K by one wave as K rounds of wave-wide argmax over the 192 scores (3
+// per lane, expert e at lane e % 64, slot e / 64), on order-preserving integer
+// keys (-0 folded into +0, so that equal floats give equal keys). While every
+// round's maximum is unique the result is the selection order of
+// topk_wave_regs; a round with a tied maximum, or a NaN anywhere, returns
+// false and the caller falls back to topk_wave_regs, which follows the
+// reference's selection with swaps in every case. Lane k < K receives the
+// k-th expert and its sigma; sum = sigma_0 + sigma_1 + ... in selection
+// order (wave-uniform). No LDS, no barrier.
+__device__ __forceinline__ bool topk_wave_fast(const float (&sc)[3], const float (&sg)[3], int K,
+                                               int &my_e, float &my_sig, float &sum) {
+#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  float sc[3], sg[3];
+  uint32_t key[3];
+  bool nan = false;
 #pragma unroll
   for (int m = 0; m < 3; m++) {
-    sc[m] = score[lane + 64 * m];
-    sg[m] = sig[lane + 64 * m];
+    nan |= sc[m] != sc[m];
+    const uint32_t u = __builtin_bit_cast(uint32_t, sc[m] + 0.0f);
+    key[m] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // > 0 for every non-NaN
   }
-  topk_wave_regs(sc, sg, K, scale, ids, wpre, wout);
-}
-
-// Top-K by a 256-thread block, with the same result as topk_wave_regs.
-// Rank of element e = number of scores strictly greater than score[e]: wave w
-// holds quarter w (scores 48w .. 48w+47) as wave-uniform values and counts,
-// for each of its lanes' three elements (lane + 64 m), how many of them are
-// greater; the four partial counts are summed in LDS. With distinct top
-// scores, selection with swaps picks in descending score order, so the
-// element of rank k is the k-th pick. Any tie among the first K ranks (two
-// elements with one rank, or a rank left empty) or a NaN sends wave 0 to the
-// sequential selection, which defines the result then.
-// sig / score: 192 entries each (global or LDS; visible to the whole block).
-// sg_l: LDS float[192]; scratch_l: LDS int[4*192 + 2*KMAX + 2]. ids_l, wpre_l,
-// w_l: outputs (LDS or global), valid after the call, which ends with a
-// barrier unless kFinalBarrier is false (then the caller's next barrier makes
-// them visible). Every thread must call it; after it, no global memory is read.
-template <bool kFinalBarrier = true>
-__device__ __forceinline__ void topk_block(const float *sig, const float *score, int K, float scale,
-                                           int32_t *ids_l, float *wpre_l, float *w_l, float *sg_l,
-                                           int32_t *scratch_l,
-                                           unsigned long long *trace = nullptr) {
-#pragma clang fp contract(off)
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int32_t *part_l = scratch_l, *cnt_l = scratch_l + 4 * E, *flag_l = cnt_l + KMAX,
-          *sel_l = flag_l + 1;
-  // every load first: the lane's three elements, the wave's quarter, sigma
-  float v[3];
-#pragma unroll
-  for (int m = 0; m < 3; m++) v[m] = score[lane + 64 * m];
-  float4 q4[12];
-  // waves past the fourth (wider blocks) repeat a quarter and keep no count
-  const float4 *qsrc = reinterpret_cast<const float4 *>(score + 48 * (wave & 3));
-#pragma unroll
-  for (int u = 0; u < 12; u++) q4[u] = qsrc[u];
-  // unconditional (a clamped index): a load under a lane condition would wait
-  // for the loads issued before it
-  const float sgv = sig[tid < E ? tid : E - 1];
-  if (tid < KMAX) cnt_l[tid] = 0;
-  if (tid == 0) *flag_l = 0;
-  int cnt[3] = {0, 0, 0};
-#pragma unroll
-  for (int u = 0; u < 12; u++) {
-    const float qx = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].x)));
-    const float qy = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].y)));
-    const float qz = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].z)));
-    const float qw = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q4[u].w)));
-#pragma unroll
-    for (int m = 0; m < 3; m++)
-      cnt[m] += (int)(qx > v[m]) + (int)(qy > v[m]) + (int)(qz > v[m]) + (int)(qw > v[m]);
-  }
-#pragma unroll
-  for (int m = 0; m < 3; m++)
-    if (wave < 4) part_l[wave * E + lane + 64 * m] = cnt[m];
-  if (tid < E) sg_l[tid] = sgv;
-  __syncthreads();
-  if (trace) trace_point(trace, 4);
-  if (tid < E) {
-    const int rank = (part_l[tid] + part_l[tid + E]) + (part_l[tid + 2 * E] + part_l[tid + 3 * E]);
-    const float sv = wave == 0 ? v[0] : (wave == 1 ? v[1] : v[2]);  // score[tid]
-    if (sv != sv) atomicOr(flag_l, 1);
-    if (rank < K) {
-      atomicAdd(&cnt_l[rank], 1);
-      sel_l[rank] = tid;
+  if (__builtin_amdgcn_ballot_w64(nan)) return false;
+  sum = 0.0f;
+  my_e = 0;
+  my_sig = 0.0f;
+  for (int k = 0; k < K; k++) {
+    uint32_t v = key[0] > key[1] ? key[0] : key[1];
+    v = v > key[2] ? v : key[2];
+    // row maxima by DPP, then the four rows
+    v = max(v, (uint32_t)dppi<DPP_XOR1>((int)v));
+    v = max(v, (uint32_t)dppi<DPP_XOR2>((int)v));
+    v = max(v, (uint32_t)dppi<DPP_HALF_MIRROR>((int)v));
+    v = max(v, (uint32_t)dppi<DPP_MIRROR>((int)v));
+    uint32_t M = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    M = max(M, (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    M = max(M, (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
+    M = max(M, (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    const uint64_t b0 = __builtin_amdgcn_ballot_w64(key[0] == M);
+    const uint64_t b1 = __builtin_amdgcn_ballot_w64(key[1] == M);
+    const uint64_t b2 = __builtin_amdgcn_ballot_w64(key[2] == M);
+    if (__builtin_popcountll(b0) + __builtin_popcountll(b1) + __builtin_popcountll(b2) != 1)
+      return false;  // a tie for this place
+    const int m = b0 ? 0 : (b1 ? 1 : 2);
+    const int wl = __builtin_ctzll(b0 | b1 | b2);
+    const float s_e = pick3_lane(sg, m, wl);
+    sum = sum + s_e;
+    if (lane == k) {
+      my_e = wl + 64 * m;
+      my_sig = s_e;
     }
+#pragma unroll
+    for (int mm = 0; mm < 3; mm++)  // taken (a static index: the keys stay in registers)
+      if (mm == m && lane == wl) key[mm] = 0u;
   }
-  __syncthreads();
-  if (tid < K && cnt_l[tid] != 1) atomicOr(flag_l, 1);
-  __syncthreads();
-  if (trace) trace_point(trace, 5);
-  if (*flag_l) {
-    if (wave == 0) topk_wave(sg_l, score, K, scale, ids_l, wpre_l, w_l);
-  } else if (wave == 0) {
-    const int e = lane < K ? sel_l[lane] : 0;
-    const float se = sg_l[e];
-    float sum = 0.0f;
-    for (int k = 0; k < K; k++)
-      sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, se), k));
-    const float inv = 1.0f / (sum + 1e-20f);
-    if (lane < K) {
-      const float wv = se * inv;
-      ids_l[lane] = e;
-      wpre_l[lane] = wv;
-      w_l[lane] = wv * scale;
-    }
-  }
-  if (kFinalBarrier) __syncthreads();
+  return true;
 }
 
 // Sum of squares of a 4096-vector by a 256-thread block, thread t holding
@@ -272,7 +237,7 @@ __device__ __forceinline__ void stage_store(__half *dst, int j, float v) {
 }
 
 // Device dispatch, step 0 (in the first kernel of the routing): clear the
-// E x ceil(T/32) token-bitmap words of step 1. Part `part` of `nparts` (one
+// E x ceil(T/32) token-bitmap words that k_topk marks. Part `part` of `nparts` (one
 // per block of that kernel) clears its share; a fill by kernels, not a
 // memset, so that the forward stays graph-capturable.
 __device__ __forceinline__ void dispatch_clear_part(int T, uint32_t *bits, int wt, int part,
@@ -282,15 +247,5 @@ __device__ __forceinline__ void dispatch_clear_part(int T, uint32_t *bits, int w
     bits[(f / nw) * wt + f % nw] = 0u;
 }
 
-// Step 1 (in the top-K kernel, once token t's ids are out): bit t of each of
-// its experts' token bitmaps (bits[e * wt + t / 32]). The result is
-// independent of the order of the atomics; step 2 counts by popcount.
-__device__ __forceinline__ void dispatch_mark(const int32_t *ids_t, int t, int K, uint32_t *bits,
-                                              int wt) {
-  if ((int)threadIdx.x < K) {
-    const int e = ids_t[threadIdx.x];
-    if (e >= 0 && e < E) atomicOr(&bits[(size_t)e * wt + (t >> 5)], 1u << (t & 31));
-  }
-}
 
 }  // namespace hy3x

@@ -368,28 +368,42 @@ template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
 template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY>(
     const float *, const float *, int, float *);
 
-// Routing of one token per block (T > 1 paths): sigmoid and scores of the
-// 192 logits, then the top-K.
+// Routing of one token per wave (T > 1 paths), a block holding 1 or 4 waves: sigmoid and
+// score of the 192 logits (expert lane + 64 m in slot m), the top-K in
+// registers (topk_wave_fast, or topk_wave_regs on a tie or NaN), then the
+// token's bit in each of its experts' dispatch bitmaps.
 __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
                                               const float *__restrict__ bias, int has_bias, int K,
                                               float scale, int T, int32_t *__restrict__ ids,
                                               float *__restrict__ wpre, float *__restrict__ wout,
                                               uint32_t *__restrict__ bits, int wt) {
-  const int t = blockIdx.x;
-  __shared__ __attribute__((aligned(16))) float sg[E], sc[E], sg_l[E];
-  __shared__ int32_t scratch_l[4 * E + 2 * KMAX + 2];
-  if (threadIdx.x < E) {
-    const int e = threadIdx.x;
-    const float v = sigmoid_c(logits[(size_t)t * E + e]);
-    sg[e] = v;
-    sc[e] = has_bias ? v + bias[e] : v;
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves
+  float sg[3], sc[3];
+#pragma unroll
+  for (int m = 0; m < 3; m++) {
+    const int e = lane + 64 * m;
+    sg[m] = sigmoid_c(logits[(size_t)t * E + e]);
+    sc[m] = has_bias ? sg[m] + bias[e] : sg[m];
   }
-  __syncthreads();
-  __shared__ int32_t ids_l[KMAX];
-  topk_block(sg, sc, K, scale, ids_l, wpre + (size_t)t * K, wout + (size_t)t * K, sg_l,
-             scratch_l);
-  if (threadIdx.x < K) ids[(size_t)t * K + threadIdx.x] = ids_l[threadIdx.x];
-  if (bits) dispatch_mark(ids_l, t, K, bits, wt);
+  int32_t *ids_t = ids + (size_t)t * K;
+  int my_e;
+  float my_sig, sum;
+  if (topk_wave_fast(sc, sg, K, my_e, my_sig, sum)) {
+    if (lane < K) {
+      const float inv = 1.0f / (sum + 1e-20f);
+      const float v = my_sig * inv;
+      ids_t[lane] = my_e;
+      wpre[(size_t)t * K + lane] = v;
+      wout[(size_t)t * K + lane] = v * scale;
+    }
+  } else {
+    topk_wave_regs(sc, sg, K, scale, ids_t, wpre + (size_t)t * K, wout + (size_t)t * K);
+    my_e = lane < K ? ids_t[lane] : 0;  // this lane's own store: program order
+  }
+  if (bits && lane < K) atomicOr(&bits[(size_t)my_e * wt + (t >> 5)], 1u << (t & 31));
 }
 
 // Device dispatch: per-expert slot lists and the work-tile list.
@@ -414,8 +428,8 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int *tmp) {
   return base + incl - v;
 }
 
-// Step 2, one block per expert (E + 1 blocks, the last is the shared expert):
-// list offset and first tile from exclusive scans of all counts, the expert's
+// Dispatch lists from the bitmaps k_topk marked, one block per expert (E + 1
+// blocks, the last is the shared expert): list offset and first tile from exclusive scans of all counts, the expert's
 // tiles, and its slots in token order from its bitmap (popcount prefix sums).
 // Block E also writes the tile count, the per-expert counts and the stats.
 __global__ __launch_bounds__(256) void k_dispatch_list(
