@@ -91,15 +91,16 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
                                                const int4 *, const int32_t *, float *);
 
 // The MFMA grouped GEMMs in two shapes (hy3x_mfma.hip, compiled once per
-// shape). A work tile has 16 WAVES gate/up rows (per matrix) or 32 WAVES down
-// rows and up to TOKENS tokens:
+// shape). A work tile has ROWS_GU = 16 WAVES RGU gate/up rows (per matrix) or
+// twice as many down rows and up to TOKENS tokens; each wave takes 16 RGU
+// gate/up rows or 32 RGU down rows:
 //   narrow: 32 tokens, 4 waves -- two workgroups per CU; the shape for few
 //           tokens per expert;
 //   wide:   64 tokens, 8 waves -- one workgroup per CU, half the per-token
 //           dequantisation work; the shape for long prefills.
-#define HY3X_DECLARE_MFMA(NS, TOK, WV)                                                        \
+#define HY3X_DECLARE_MFMA(NS, TOK, WV, RGU_)                                                  \
   namespace NS {                                                                            \
-  constexpr int TOKENS = TOK, WAVES = WV;                                                   \
+  constexpr int TOKENS = TOK, WAVES = WV, RGU = RGU_, ROWS_GU = 16 * WV * RGU_;             \
   template <bool GATEUP>                                                                    \
   __global__ __launch_bounds__(64 * WV) void k_moe_mfma(                                    \
       const uint8_t *wq, const uint8_t *wsh, const __half *act, const __half *act_sum,      \
@@ -112,8 +113,14 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
       const uint8_t *, const uint8_t *, const __half *, const __half *, const int32_t *,    \
       const int4 *, const int32_t *, int, int, __half *, float *);                          \
   }
-HY3X_DECLARE_MFMA(mfma_narrow, 32, 4)
-HY3X_DECLARE_MFMA(mfma_wide, 64, 8)
+#ifndef HY3X_WIDE_WAVES
+#define HY3X_WIDE_WAVES 8
+#endif
+#ifndef HY3X_WIDE_RGU
+#define HY3X_WIDE_RGU 1
+#endif
+HY3X_DECLARE_MFMA(mfma_narrow, 32, 4, 1)
+HY3X_DECLARE_MFMA(mfma_wide, 64, HY3X_WIDE_WAVES, HY3X_WIDE_RGU)
 #undef HY3X_DECLARE_MFMA
 __global__ void k_stage_mfma(const float *s32, __half *s16m, __half *ssum);
 __global__ void k_hsums(const __half *h16m, __half *hsum);

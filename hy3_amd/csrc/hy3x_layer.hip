@@ -371,12 +371,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                           L->stats, L->h16, L->trace[1]);
       else if (c.mode == Mode::MFMA && c.wide)
         mfma_wide::k_moe_mfma<true>
-            <<<mt * (F / (16 * mfma_wide::WAVES)), 64 * mfma_wide::WAVES, 0, st>>>(
+            <<<mt * (F / mfma_wide::ROWS_GU), 64 * mfma_wide::WAVES, 0, st>>>(
                 L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list, L->tiles,
                 L->n_tiles, T, K, L->h16m, nullptr);
       else if (c.mode == Mode::MFMA)
         mfma_narrow::k_moe_mfma<true>
-            <<<mt * (F / (16 * mfma_narrow::WAVES)), 64 * mfma_narrow::WAVES, 0, st>>>(
+            <<<mt * (F / mfma_narrow::ROWS_GU), 64 * mfma_narrow::WAVES, 0, st>>>(
                 L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list, L->tiles,
                 L->n_tiles, T, K, L->h16m, nullptr);
       else
@@ -393,12 +393,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         const uint8_t *wsh = L->shared_q8 ? L->wsh : nullptr;
         if (c.wide)
           mfma_wide::k_moe_mfma<false>
-              <<<mt * (D / (32 * mfma_wide::WAVES)), 64 * mfma_wide::WAVES, 0, st>>>(
+              <<<mt * (D / (2 * mfma_wide::ROWS_GU)), 64 * mfma_wide::WAVES, 0, st>>>(
                   L->wq, wsh, L->h16m, L->hsum, L->list, L->tiles, L->n_tiles, T, K, nullptr,
                   L->out);
         else
           mfma_narrow::k_moe_mfma<false>
-              <<<mt * (D / (32 * mfma_narrow::WAVES)), 64 * mfma_narrow::WAVES, 0, st>>>(
+              <<<mt * (D / (2 * mfma_narrow::ROWS_GU)), 64 * mfma_narrow::WAVES, 0, st>>>(
                   L->wq, wsh, L->h16m, L->hsum, L->list, L->tiles, L->n_tiles, T, K, nullptr,
                   L->out);
       }

@@ -61,8 +61,9 @@ constexpr int MT_TOK = TOKENS;             // tokens per tile (dispatch NT for t
 static_assert(MT_TOK == 32 || MT_TOK == 64, "tile tokens");
 constexpr int MT_WAVES = WAVES;            // waves per workgroup
 constexpr int MT_THREADS = 64 * MT_WAVES;
-constexpr int RB = 32 * MT_WAVES;          // row-blocks per tile and block column
-constexpr int RB_HALF = 16 * MT_WAVES;     // gate/up: gate row-blocks, then up
+constexpr int MT_RGU = RGU;                // 16-row gate/up groups per wave (down: twice)
+constexpr int RB = 32 * MT_WAVES * MT_RGU; // row-blocks per tile and block column
+constexpr int RB_HALF = RB / 2;            // gate/up: gate row-blocks, then up
 constexpr int RB_CHUNKS = 9;    // 16-byte chunks per row-block (144 B)
 constexpr int A_CHUNKS = RB * RB_CHUNKS;              // 2304 per column
 constexpr int A_CHUNKS_WAVE = A_CHUNKS / MT_WAVES;    // 288 per wave (32 row-blocks)
@@ -167,7 +168,7 @@ template <bool GATEUP>
 struct MfmaCfg {
   static constexpr int KD = GATEUP ? D : F;        // reduction length
   static constexpr int NROWS = GATEUP ? F : D;     // weight rows
-  static constexpr int RG = GATEUP ? 1 : 2;        // 16-row groups per wave
+  static constexpr int RG = GATEUP ? MT_RGU : 2 * MT_RGU;  // 16-row groups per wave
   static constexpr int TROWS = 16 * MT_WAVES * RG; // weight rows per tile
   static constexpr int NRT = NROWS / TROWS;        // row tiles
   static constexpr int NKB = KD / QK;              // Q4_K block columns (16 / 6)
@@ -276,7 +277,7 @@ __device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
   for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
-      const int rb = GATEUP ? m * RB_HALF + 16 * wave + lr : 16 * (2 * wave + rg) + lr;
+      const int rb = (GATEUP ? m * RB_HALF : 0) + 16 * (RG * wave + rg) + lr;
       hdr[rg][m] = as[rb * RB_CHUNKS];
       pv[rg][m][0] = as[rb * RB_CHUNKS + 1 + g];
       pv[rg][m][1] = as[rb * RB_CHUNKS + 5 + g];
@@ -357,7 +358,7 @@ __device__ __forceinline__ void store_tile(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int rg = 0; rg < C::RG; rg++) {
-    const int r = rt * C::TROWS + 16 * (GATEUP ? wave : 2 * wave + rg) + lr;
+    const int r = rt * C::TROWS + 16 * (C::RG * wave + rg) + lr;
 #pragma unroll
     for (int t = 0; t < NTT; t++)
 #pragma unroll
@@ -512,7 +513,7 @@ __device__ __forceinline__ void mfma_step_q8(TileStateQ8<GATEUP, NTT> &st, int k
   for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
-      const int rb = GATEUP ? m * RB_HALF + 16 * wave + lr : 16 * (2 * wave + rg) + lr;
+      const int rb = (GATEUP ? m * RB_HALF : 0) + 16 * (RG * wave + rg) + lr;
       dsc[rg][m] = __builtin_bit_cast(f4_t, as[rb * RB_CHUNKS]);
       const u2_t *qp = reinterpret_cast<const u2_t *>(as + rb * RB_CHUNKS + 1);
 #pragma unroll
