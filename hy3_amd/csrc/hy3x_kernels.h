@@ -38,13 +38,13 @@ constexpr int ROUTER_R_TINY = HY3X_ROUTER_R_TINY, ROUTER_R_MID = HY3X_ROUTER_R_M
 template <int MT, int ME, int TG, int EG, int KC, int R>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
                                                      float *logits);
-extern template __global__ void k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
-    const float *, const float *, int, float *);
 extern template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
     const float *, const float *, int, float *);
 extern template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
     const float *, const float *, int, float *);
 extern template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY>(
+    const float *, const float *, int, float *);
+extern template __global__ void k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
     const float *, const float *, int, float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
                        int T, int32_t *ids, float *wpre, float *wout, uint32_t *bits, int wt);

@@ -124,10 +124,18 @@ constexpr int kSmallRouterT = HY3X_SMALL_ROUTER_T;
 #define HY3X_TINY_ROUTER_T 64
 #endif
 constexpr int kTinyRouterT = HY3X_TINY_ROUTER_T;
-// Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks).
-constexpr int kMidRouterT = 128;
+// Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks;
+// at T = 256, 41 vs 54 us for the router stage with the next size), then up to
+// kLargeRouterT 16 x 16 tiles (4 x 2 per thread: at T = 512, 384 blocks).
+#ifndef HY3X_MID_ROUTER_T
+#define HY3X_MID_ROUTER_T 256
+#endif
+constexpr int kMidRouterT = HY3X_MID_ROUTER_T;
 // Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
-constexpr int kLargeRouterT = 512;
+#ifndef HY3X_LARGE_ROUTER_T
+#define HY3X_LARGE_ROUTER_T 512
+#endif
+constexpr int kLargeRouterT = HY3X_LARGE_ROUTER_T;
 // From this many tokens the experts run as MFMA grouped GEMMs. Measured on MI355X the
 // MFMA tiles beat the wavefront-reduction GEMV tiles at every T >= 2 (T=2: 51 vs 66 us,
 // T=32: 442 vs 550 us for gate/up + down), so the GEMV tiles only run when selected
@@ -340,7 +348,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
           k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else if (T <= kLargeRouterT)
-          k_router_gemm<4, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 15) / 16, E / 32), 256, 0, st>>>(
+          k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 15) / 16, E / 16), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else
           k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
