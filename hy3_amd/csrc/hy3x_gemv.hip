@@ -197,7 +197,11 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
   // every wave and block, so the outcome is block-uniform)
   int my_e;
   float my_sig, sum;
-  const bool fast = topk_wave_fast(sc, sg, K, my_e, my_sig, sum);
+  // a block needs the first slot + 1 places only (block 0, which publishes
+  // the routing, all K): places before a tie are the same in every method.
+  // (Issuing the first weight loads before the activation reads below, as
+  // the shared-expert blocks do, measured 4 us slower here.)
+  const bool fast = topk_wave_fast(sc, sg, blockIdx.x == 0 ? K : slot + 1, my_e, my_sig, sum);
   __syncthreads();  // s_l staged
   int e;
   if (fast) {

@@ -156,7 +156,9 @@ __device__ __forceinline__ void topk_wave_regs(const float (&sc)[3], const float
 // false and the caller falls back to topk_wave_regs, which follows the
 // reference's selection with swaps in every case. Lane k < K receives the
 // k-th expert and its sigma; sum = sigma_0 + sigma_1 + ... in selection
-// order (wave-uniform). No LDS, no barrier.
+// order (wave-uniform). K may be smaller than the routing's top-K when only
+// the first places are needed: they do not depend on the later ones. No LDS,
+// no barrier.
 __device__ __forceinline__ bool topk_wave_fast(const float (&sc)[3], const float (&sg)[3], int K,
                                                int &my_e, float &my_sig, float &sum) {
 #pragma clang fp contract(off)
