@@ -175,36 +175,46 @@ __device__ __forceinline__ bool topk_wave_fast(const float (&sc)[3], const float
   sum = 0.0f;
   my_e = 0;
   my_sig = 0.0f;
+  bool tie = false;
   for (int k = 0; k < K; k++) {
     uint32_t v = key[0] > key[1] ? key[0] : key[1];
     v = v > key[2] ? v : key[2];
-    // row maxima by DPP, then the four rows
+    // row maxima by DPP, then row 0 into row 1 and row 2 into row 3
+    // (row_bcast:15), then lane 31 into rows 2 and 3 (row_bcast:31): lane 63
+    // holds the wave maximum
     v = max(v, (uint32_t)dppi<DPP_XOR1>((int)v));
     v = max(v, (uint32_t)dppi<DPP_XOR2>((int)v));
     v = max(v, (uint32_t)dppi<DPP_HALF_MIRROR>((int)v));
     v = max(v, (uint32_t)dppi<DPP_MIRROR>((int)v));
-    uint32_t M = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-    M = max(M, (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
-    M = max(M, (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
-    M = max(M, (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
-    const uint64_t b0 = __builtin_amdgcn_ballot_w64(key[0] == M);
-    const uint64_t b1 = __builtin_amdgcn_ballot_w64(key[1] == M);
-    const uint64_t b2 = __builtin_amdgcn_ballot_w64(key[2] == M);
-    if (__builtin_popcountll(b0) + __builtin_popcountll(b1) + __builtin_popcountll(b2) != 1)
-      return false;  // a tie for this place
-    const int m = b0 ? 0 : (b1 ? 1 : 2);
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, DPP_BCAST15, 0xA, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, DPP_BCAST31, 0xC, 0xF, false));
+    const uint32_t M = (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+    const bool h0 = key[0] == M, h1 = key[1] == M, h2 = key[2] == M;
+    const uint64_t b0 = __builtin_amdgcn_ballot_w64(h0);
+    const uint64_t b1 = __builtin_amdgcn_ballot_w64(h1);
+    const uint64_t b2 = __builtin_amdgcn_ballot_w64(h2);
+    // a tie for this place: noted, the rounds go on without a branch
+    tie |= __builtin_popcountll(b0) + __builtin_popcountll(b1) + __builtin_popcountll(b2) != 1;
     const int wl = __builtin_ctzll(b0 | b1 | b2);
-    const float s_e = pick3_lane(sg, m, wl);
+    // the winner's slot and sigma, chosen in its own lane, then read out once
+    // (masked ORs of the three values, not a select between array elements,
+    // which the compiler lowers to an indexed memory read)
+    const uint32_t sel_sig = (h0 ? __builtin_bit_cast(uint32_t, sg[0]) : 0u) |
+                             (h1 ? __builtin_bit_cast(uint32_t, sg[1]) : 0u) |
+                             (h2 ? __builtin_bit_cast(uint32_t, sg[2]) : 0u);
+    const int sel_e = lane + (h1 ? 64 : 0) + (h2 ? 128 : 0);
+    const float s_e = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)sel_sig, wl));
+    const int e_w = __builtin_amdgcn_readlane(sel_e, wl);
     sum = sum + s_e;
     if (lane == k) {
-      my_e = wl + 64 * m;
+      my_e = e_w;
       my_sig = s_e;
     }
-#pragma unroll
-    for (int mm = 0; mm < 3; mm++)  // taken (a static index: the keys stay in registers)
-      if (mm == m && lane == wl) key[mm] = 0u;
+    key[0] = h0 ? 0u : key[0];  // taken
+    key[1] = h1 ? 0u : key[1];
+    key[2] = h2 ? 0u : key[2];
   }
-  return true;
+  return !tie;
 }
 
 // Sum of squares of a 4096-vector by a 256-thread block, thread t holding
