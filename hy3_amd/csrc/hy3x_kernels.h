@@ -20,7 +20,11 @@ __global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w
 #ifndef HY3X_ROUTER_KC_LARGE
 #define HY3X_ROUTER_KC_LARGE 128
 #endif
-constexpr int ROUTER_KC_MID = HY3X_ROUTER_KC_MID, ROUTER_KC_LARGE = HY3X_ROUTER_KC_LARGE;
+#ifndef HY3X_ROUTER_KC_TINY
+#define HY3X_ROUTER_KC_TINY 256
+#endif
+constexpr int ROUTER_KC_MID = HY3X_ROUTER_KC_MID, ROUTER_KC_LARGE = HY3X_ROUTER_KC_LARGE,
+              ROUTER_KC_TINY = HY3X_ROUTER_KC_TINY;
 // K chunks in flight (register ring) per tile size: few blocks run at small T,
 // so each chunk's load latency must hide behind the previous chunks' FMAs.
 #ifndef HY3X_ROUTER_R_TINY
@@ -42,7 +46,7 @@ extern template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_
     const float *, const float *, int, float *);
 extern template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
     const float *, const float *, int, float *);
-extern template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY>(
+extern template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY>(
     const float *, const float *, int, float *);
 extern template __global__ void k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
     const float *, const float *, int, float *);

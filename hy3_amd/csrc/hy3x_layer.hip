@@ -342,7 +342,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : L->s16, L->s32,
                                      mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt);
         if (T <= kTinyRouterT)
-          k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
+          k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
         else if (T <= kMidRouterT)
           k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(

@@ -367,7 +367,7 @@ template __global__ void k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LAR
     const float *, const float *, int, float *);
 template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
     const float *, const float *, int, float *);
-template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_MID, ROUTER_R_TINY>(
+template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY>(
     const float *, const float *, int, float *);
 
 // Routing of one token per wave (T > 1 paths), a block holding 1 or 4 waves: sigmoid and
