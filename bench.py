@@ -283,7 +283,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md, not implemented.", file=sys.stderr)
+              "multi-GPU sharding (expert or tensor parallel) is not implemented.", file=sys.stderr)
         sys.exit(2)
     import torch
     if a.copy_calibration:
