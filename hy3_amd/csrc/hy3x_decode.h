@@ -118,7 +118,10 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
 #ifndef HY3X_GU_PF
 #define HY3X_GU_PF 4
 #endif
-constexpr int DEC_RPW = 4;                   // gate/up rows per wave
+#ifndef HY3X_GU_RPW
+#define HY3X_GU_RPW 4
+#endif
+constexpr int DEC_RPW = HY3X_GU_RPW;         // gate/up rows per wave
 constexpr int DEC_GU_PF = HY3X_GU_PF;        // gate/up rows in flight per wave
 constexpr int DEC_RPB = 4 * DEC_RPW;         // shared gate/up rows per routing block (four waves)
 constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (96)
