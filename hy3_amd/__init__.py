@@ -58,8 +58,10 @@ _SIGS = {
     "hy3x_synth_quantize_q8_0": (I32, [P, P, I64, P]),
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
     "hy3x_layer_forward_residual": (I32, [P, P, P, I32, I32, F32, P]),
-    "hy3x_layer_last_routing": (I32, [P, P, P, P]),
+    "hy3x_layer_last_routing": (I32, [P, P, P, P, I64]),
+    "hy3x_layer_last_shape": (I32, [P, ctypes.POINTER(I32), ctypes.POINTER(I32)]),
     "hy3x_layer_set_path": (I32, [P, I32]),
+    "hy3x_layer_set_rms_scale": (I32, [P, P, I32]),
     "hy3x_layer_last_path": (I32, [P, ctypes.POINTER(ctypes.c_int)]),
     "hy3x_layer_time_stage": (I32, [P, I32, I32, P, ctypes.POINTER(ctypes.c_float)]),
     "hy3x_diag_read_rate": (I32, [P, I64, I64, I32, P, ctypes.POINTER(ctypes.c_float)]),
@@ -220,6 +222,14 @@ class MoELayer:
         _check(lib().hy3x_layer_last_path(self._h, ctypes.byref(v)))
         return v.value
 
+    def set_rms_scale(self, r=None):
+        """Substitute the per-token RMSNorm scale (None: compute it again)."""
+        if r is None:
+            _check(lib().hy3x_layer_set_rms_scale(self._h, None, 0))
+            return
+        r = np.ascontiguousarray(r, np.float32).ravel()
+        _check(lib().hy3x_layer_set_rms_scale(self._h, r.ctypes.data, r.size))
+
     STAGES = ("router", "dispatch", "gateup", "down", "combine")
 
     def set_timing(self, enable):
@@ -256,10 +266,22 @@ class MoELayer:
         _check(lib().hy3x_layer_forward_residual(self._h, x_dev_ptr, attn_dev_ptr, T, K, scale,
                                                  stream))
 
-    def last_routing(self, T, K):
-        ids = np.empty((T, K), np.int32)
-        wpre = np.empty((T, K), np.float32)
-        w = np.empty((T, K), np.float32)
+    def last_shape(self):
+        """(T, K) of the last forward."""
+        t, k = I32(), I32()
+        _check(lib().hy3x_layer_last_shape(self._h, ctypes.byref(t), ctypes.byref(k)))
+        return t.value, k.value
+
+    def last_routing(self, T=None, K=None):
+        """ids, wpre, w of the last forward, each [T x K]. T and K, when given, must be
+        the last forward's (they are checked; the buffers are sized from the library's
+        own record)."""
+        t, k = self.last_shape()
+        if (T is not None and T != t) or (K is not None and K != k):
+            raise HY3XError(f"last forward was T={t}, K={k}, not T={T}, K={K}")
+        ids = np.empty((t, k), np.int32)
+        wpre = np.empty((t, k), np.float32)
+        w = np.empty((t, k), np.float32)
         _check(lib().hy3x_layer_last_routing(self._h, ids.ctypes.data, wpre.ctypes.data,
-                                             w.ctypes.data))
+                                             w.ctypes.data, ids.size))
         return ids, wpre, w

@@ -14,8 +14,6 @@ hy3_amd/libhy3x.so. Flags:
                                             copies between accumulation and
                                             vector registers around the
                                             per-block scale FMAs).
-HY3X_EXTRA_FLAGS (environment) appends flags, e.g. the tile-shape macros of
-hy3x_mfma.hip for tuning runs.
 """
 import os
 import subprocess
@@ -35,7 +33,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-] + os.environ.get("HY3X_EXTRA_FLAGS", "").split()  # e.g. "-DHY3X_MFMA_WAVES=8" (tuning runs)
+]
 
 
 def sources():

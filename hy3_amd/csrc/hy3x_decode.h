@@ -114,33 +114,20 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
   }
 }
 
-// Decode launch shapes.
-#ifndef HY3X_GU_PF
-#define HY3X_GU_PF 4
-#endif
-#ifndef HY3X_GU_RPW
-#define HY3X_GU_RPW 4
-#endif
-constexpr int DEC_RPW = HY3X_GU_RPW;         // gate/up rows per wave
-constexpr int DEC_GU_PF = HY3X_GU_PF;        // gate/up rows in flight per wave
+// Decode launch shapes (measured on MI355X; the alternatives tried and their
+// figures are recorded with the design notes, not as build switches).
+constexpr int DEC_RPW = 4;                   // gate/up rows per wave
+constexpr int DEC_GU_PF = 4;                 // gate/up rows in flight per wave
 constexpr int DEC_RPB = 4 * DEC_RPW;         // shared gate/up rows per routing block (four waves)
+static_assert(F % DEC_RPB == 0, "the routing kernel's shared blocks cover every row");
 constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (96)
 // Waves per routed gate/up block (each block routes the token once, then its
 // waves stream DEC_RPW rows each).
-#ifndef HY3X_GU_WAVES
-#define HY3X_GU_WAVES 4
-#endif
-constexpr int DEC_GU_WAVES = HY3X_GU_WAVES;
+constexpr int DEC_GU_WAVES = 4;
 constexpr int DEC_GU_RPB = DEC_GU_WAVES * DEC_RPW;  // routed gate/up rows per block
 static_assert(F % DEC_GU_RPB == 0, "whole blocks per expert");
 constexpr int DEC_GU_BLOCKS = F / DEC_GU_RPB;       // routed gate/up blocks per expert
-#ifndef HY3X_DOWN_RPB
-#define HY3X_DOWN_RPB 16
-#endif
-#ifndef HY3X_DOWN_PF
-#define HY3X_DOWN_PF 2
-#endif
-constexpr int DEC_DOWN_RPB = HY3X_DOWN_RPB;  // down rows per block
-constexpr int DEC_DOWN_PF = HY3X_DOWN_PF;    // down passes (2 rows each) in flight per wave
+constexpr int DEC_DOWN_RPB = 16;  // down rows per block
+constexpr int DEC_DOWN_PF = 2;    // down passes (2 rows each) in flight per wave
 
 }  // namespace hy3x

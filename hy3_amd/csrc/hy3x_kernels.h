@@ -8,37 +8,18 @@ __global__ void k_router_logits(const float *x, const float *xadd, const float *
                                 const float *router,
                                 const float *bias, int has_bias, float *logits, float *sig,
                                 float *score, __half *s16, float *s32,
-                                unsigned long long *trace, int T, uint32_t *bits, int wt);
+                                unsigned long long *trace, int T, uint32_t *bits, int wt,
+                                const float *r_in);
 __global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w, __half *s16,
                           float *s32,
-                          __half *s16m, __half *ssum, int T, uint32_t *bits, int wt);
-// K chunk of the router GEMM: small and mid-size tiles (4 x 8 and 8 x 16
-// tokens x experts) and the larger ones. Tuning macros.
-#ifndef HY3X_ROUTER_KC_MID
-#define HY3X_ROUTER_KC_MID 256
-#endif
-#ifndef HY3X_ROUTER_KC_LARGE
-#define HY3X_ROUTER_KC_LARGE 128
-#endif
-#ifndef HY3X_ROUTER_KC_TINY
-#define HY3X_ROUTER_KC_TINY 256
-#endif
-constexpr int ROUTER_KC_MID = HY3X_ROUTER_KC_MID, ROUTER_KC_LARGE = HY3X_ROUTER_KC_LARGE,
-              ROUTER_KC_TINY = HY3X_ROUTER_KC_TINY;
-// K chunks in flight (register ring) per tile size: few blocks run at small T,
-// so each chunk's load latency must hide behind the previous chunks' FMAs.
-#ifndef HY3X_ROUTER_R_TINY
-#define HY3X_ROUTER_R_TINY 2
-#endif
-#ifndef HY3X_ROUTER_R_MID
-#define HY3X_ROUTER_R_MID 2
-#endif
-
-#ifndef HY3X_ROUTER_R_LARGE
-#define HY3X_ROUTER_R_LARGE 1
-#endif
-constexpr int ROUTER_R_TINY = HY3X_ROUTER_R_TINY, ROUTER_R_MID = HY3X_ROUTER_R_MID,
-              ROUTER_R_LARGE = HY3X_ROUTER_R_LARGE;
+                          __half *s16m, __half *ssum, int T, uint32_t *bits, int wt,
+                          const float *r_in);
+// K chunk of the router GEMM (floats per LDS stage) and chunks in flight
+// (register ring) per tile size: 4 x 8 (tiny), 8 x 16 (mid) and the larger
+// tiles. Few blocks run at small T, so each chunk's load latency must hide
+// behind the previous chunks' FMAs.
+constexpr int ROUTER_KC_TINY = 256, ROUTER_KC_MID = 256, ROUTER_KC_LARGE = 128;
+constexpr int ROUTER_R_TINY = 2, ROUTER_R_MID = 2, ROUTER_R_LARGE = 1;
 template <int MT, int ME, int TG, int EG, int KC, int R>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
                                                      float *logits);
@@ -72,7 +53,7 @@ __global__ void k_route_decode(const float *x, const float *xadd, const float *n
                                const float *bias, int has_bias, int K, float *logits,
                                float *sig, float *score, __half *s16, float *s32,
                                const uint8_t *wq, const uint8_t *wsh, __half *h16,
-                               unsigned long long *trace);
+                               unsigned long long *trace, const float *r_in);
 __global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *ids,
                               const float *w, int K, float *x, const float *xadd,
                               const uint8_t *wsh,
@@ -117,14 +98,8 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
       const uint8_t *, const uint8_t *, const __half *, const __half *, const int32_t *,    \
       const int4 *, const int32_t *, int, int, __half *, float *);                          \
   }
-#ifndef HY3X_WIDE_WAVES
-#define HY3X_WIDE_WAVES 8
-#endif
-#ifndef HY3X_WIDE_RGU
-#define HY3X_WIDE_RGU 1
-#endif
 HY3X_DECLARE_MFMA(mfma_narrow, 32, 4, 1)
-HY3X_DECLARE_MFMA(mfma_wide, 64, HY3X_WIDE_WAVES, HY3X_WIDE_RGU)
+HY3X_DECLARE_MFMA(mfma_wide, 64, 8, 1)
 #undef HY3X_DECLARE_MFMA
 __global__ void k_stage_mfma(const float *s32, __half *s16m, __half *ssum);
 __global__ void k_hsums(const __half *h16m, __half *hsum);

@@ -43,6 +43,8 @@ struct hy3x_layer {
   uint32_t *bits = nullptr;    // dispatch: per-expert token bitmaps [E][wt]
   int wt = 0;                  // bitmap words per expert (max_tokens / 32, rounded up to 4)
   unsigned long long *stats = nullptr;
+  float *rms_r = nullptr;      // diagnostics: RMSNorm scales substituted per token
+  int rms_n = 0;               // tokens rms_r covers (0: compute r)
   int max_tiles_alloc = 0;
   int last_T = 0, last_K = 0;
   struct Forward {  // launch parameters of the current / last forward
@@ -52,6 +54,7 @@ struct hy3x_layer {
     float scale = 1.0f;
     Mode mode = Mode::GEMV;
     bool wide = false;  // MFMA mode: the wide tile shape (mfma_wide)
+    const float *r_in = nullptr;  // substituted RMSNorm scales, or null
   } cur;
   hipStream_t last_stream = nullptr;
   int path = 0;
@@ -102,6 +105,19 @@ int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
                   __FILE__, __LINE__);                                                 \
   } while (0)
 
+// Two timing events, destroyed on every return path.
+struct EventPair {
+  hipEvent_t a = nullptr, b = nullptr;
+  ~EventPair() {
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+  }
+  hipError_t create() {
+    hipError_t e = hipEventCreate(&a);
+    return e != hipSuccess ? e : hipEventCreate(&b);
+  }
+};
+
 template <class P>
 static int dalloc(P **p, size_t bytes) {
   if (hipMalloc((void **)p, bytes) != hipSuccess) {
@@ -114,28 +130,16 @@ static int dalloc(P **p, size_t bytes) {
 
 // Up to this many tokens the router runs as one wave per (expert, token);
 // above it as RMSNorm + LDS-tiled GEMM + per-token top-K.
-#ifndef HY3X_SMALL_ROUTER_T
-#define HY3X_SMALL_ROUTER_T 8
-#endif
-constexpr int kSmallRouterT = HY3X_SMALL_ROUTER_T;
+constexpr int kSmallRouterT = 8;
 // Up to this many tokens the router GEMM uses 4 x 8 block tiles, one output per thread
 // group (the most blocks: at T = 32, 192 of them).
-#ifndef HY3X_TINY_ROUTER_T
-#define HY3X_TINY_ROUTER_T 64
-#endif
-constexpr int kTinyRouterT = HY3X_TINY_ROUTER_T;
+constexpr int kTinyRouterT = 64;
 // Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks;
 // at T = 256, 41 vs 54 us for the router stage with the next size), then up to
 // kLargeRouterT 16 x 16 tiles (4 x 2 per thread: at T = 512, 384 blocks).
-#ifndef HY3X_MID_ROUTER_T
-#define HY3X_MID_ROUTER_T 256
-#endif
-constexpr int kMidRouterT = HY3X_MID_ROUTER_T;
+constexpr int kMidRouterT = 256;
 // Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
-#ifndef HY3X_LARGE_ROUTER_T
-#define HY3X_LARGE_ROUTER_T 512
-#endif
-constexpr int kLargeRouterT = HY3X_LARGE_ROUTER_T;
+constexpr int kLargeRouterT = 512;
 // From this many tokens the experts run as MFMA grouped GEMMs. Measured on MI355X the
 // MFMA tiles beat the wavefront-reduction GEMV tiles at every T >= 2 (T=2: 51 vs 66 us,
 // T=32: 442 vs 550 us for gate/up + down), so the GEMV tiles only run when selected
@@ -146,10 +150,7 @@ constexpr int kMfmaMinT = 2;
 // 128: 0.43 vs 0.48, 256: 0.51 vs 0.56, 384: 0.60 vs 0.60, 512: 0.69 vs 0.65,
 // 4096 (Zipf routing): 3.36 vs 2.62 -- with few tokens per expert the tiles are
 // mostly empty and one workgroup per CU hides less latency than two.
-#ifndef HY3X_MFMA_WIDE_MIN_T
-#define HY3X_MFMA_WIDE_MIN_T 384
-#endif
-constexpr int kMfmaWideMinT = HY3X_MFMA_WIDE_MIN_T;
+constexpr int kMfmaWideMinT = 384;
 
 static int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
@@ -169,7 +170,7 @@ int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
   void *ptrs[] = {L->wq, L->wsh, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
                   L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m, L->ssum, L->hsum, L->h16,     L->ids,     L->list,
-                  L->n_tiles, L->counts, L->tiles, L->bits, L->stats};
+                  L->n_tiles, L->counts, L->tiles, L->bits, L->stats, L->rms_r};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   for (hipEvent_t ev : L->ev_pool) (void)hipEventDestroy(ev);
@@ -183,7 +184,10 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
   if (max_tokens < 1 || max_tokens > (1 << 16))
     return fail(HY3X_E_ARG, "max_tokens %d out of range [1, 65536]", max_tokens);
   hy3x_layer *L = new hy3x_layer();
-  HIP_TRY(hipGetDevice(&L->device));
+  if (hipGetDevice(&L->device) != hipSuccess) {
+    delete L;
+    return fail(HY3X_E_HIP, "hipGetDevice failed");
+  }
   L->max_tokens = max_tokens;
   const size_t T = (size_t)max_tokens, slots = T * (KMAX + 1);
   L->max_tiles_alloc = max_tiles_for(max_tokens, KMAX, 1);
@@ -302,6 +306,18 @@ int hy3x_layer_set_shared_q8_0(hy3x_layer *L, const void *gate, const void *up, 
   return rc;
 }
 
+int hy3x_layer_set_rms_scale(hy3x_layer *L, const float *r, int n) {
+  if (!L || n < 0 || n > L->max_tokens || (n && !r))
+    return fail(HY3X_E_ARG, "bad RMSNorm scale override");
+  if (n && !L->rms_r) {
+    int rc = dalloc(&L->rms_r, (size_t)L->max_tokens * sizeof(float));
+    if (rc) return rc;
+  }
+  if (n) HIP_TRY(hipMemcpy(L->rms_r, r, (size_t)n * sizeof(float), hipMemcpyHostToDevice));
+  L->rms_n = n;
+  return HY3X_OK;
+}
+
 int hy3x_layer_set_path(hy3x_layer *L, int path) {
   if (!L || path < 0 || path > 4) return fail(HY3X_E_ARG, "bad path");
   L->path = path;
@@ -327,7 +343,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       if (c.mode == Mode::DECODE) {
         k_route_decode<<<E + DEC_SH_BLOCKS, 256, 0, st>>>(
             x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
-            L->s16, L->s32, L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16, L->trace[0]);
+            L->s16, L->s32, L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16, L->trace[0], c.r_in);
         break;
       }
       // the routing kernels also clear (first kernel) and fill (top-K) the
@@ -336,11 +352,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, c.xadd, L->norm_w, L->router, L->bias,
                                                     L->has_bias, L->logits, L->sig, L->score,
                                                     L->s16, L->s32, L->trace[0], T, L->bits,
-                                                    L->wt);
+                                                    L->wt, c.r_in);
       } else {
         const bool mf = c.mode == Mode::MFMA;
         k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : L->s16, L->s32,
-                                     mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt);
+                                     mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt,
+                                     c.r_in);
         if (T <= kTinyRouterT)
           k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
               L->s32, L->router, T, L->logits);
@@ -430,7 +447,12 @@ int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void 
 int hy3x_layer_forward_residual(hy3x_layer *L, float *x, const float *attn_out, int T, int K,
                                 float scale, void *stream) {
   if (!attn_out) return fail(HY3X_E_ARG, "NULL attn_out");
-  if (attn_out == x) return fail(HY3X_E_ARG, "attn_out must not alias x");
+  if (x && T > 0) {
+    // the kernels read x and attn_out through restrict pointers: no overlap at all
+    const uintptr_t a0 = (uintptr_t)x, b0 = (uintptr_t)attn_out;
+    const uintptr_t n = (uintptr_t)T * D * sizeof(float);
+    if (a0 < b0 + n && b0 < a0 + n) return fail(HY3X_E_ARG, "attn_out overlaps x");
+  }
   return forward_impl(L, x, attn_out, T, K, scale, stream);
 }
 
@@ -447,6 +469,7 @@ static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K
   c.T = T;
   c.K = K;
   c.scale = scale;
+  c.r_in = L->rms_n >= T ? L->rms_r : nullptr;
   if (T == 1 && L->path == 0)
     c.mode = Mode::DECODE;
   else if (L->path >= 2 || (L->path == 0 && T >= kMfmaMinT))
@@ -481,17 +504,14 @@ int hy3x_layer_time_stage(hy3x_layer *L, int stage, int reps, void *stream, floa
     return fail(HY3X_E_ARG, "stage %d outside [0,4]", stage);
   if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
   hipStream_t st = (hipStream_t)stream;
-  hipEvent_t e0, e1;
-  HIP_TRY(hipEventCreate(&e0));
-  HIP_TRY(hipEventCreate(&e1));
-  HIP_TRY(hipEventRecord(e0, st));
+  EventPair ev;
+  HIP_TRY(ev.create());
+  HIP_TRY(hipEventRecord(ev.a, st));
   for (int i = 0; i < reps; i++) launch_stage(L, stage, st);
-  HIP_TRY(hipEventRecord(e1, st));
-  HIP_TRY(hipEventSynchronize(e1));
+  HIP_TRY(hipEventRecord(ev.b, st));
+  HIP_TRY(hipEventSynchronize(ev.b));
   float ms = 0.0f;
-  HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
-  HIP_TRY(hipEventDestroy(e0));
-  HIP_TRY(hipEventDestroy(e1));
+  HIP_TRY(hipEventElapsedTime(&ms, ev.a, ev.b));
   HIP_TRY(hipGetLastError());
   *us = ms * 1e3f / reps;
   return HY3X_OK;
@@ -539,11 +559,23 @@ int hy3x_layer_set_trace(hy3x_layer *L, int stage, void *buf) {
   return HY3X_OK;
 }
 
-int hy3x_layer_last_routing(hy3x_layer *L, int32_t *ids, float *wpre, float *w) {
+int hy3x_layer_last_shape(const hy3x_layer *L, int *T, int *K) {
+  if (!L || !T || !K) return fail(HY3X_E_ARG, "NULL argument");
+  if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
+  *T = L->last_T;
+  *K = L->last_K;
+  return HY3X_OK;
+}
+
+int hy3x_layer_last_routing(hy3x_layer *L, int32_t *ids, float *wpre, float *w,
+                            int64_t capacity) {
   if (!L) return fail(HY3X_E_ARG, "NULL layer");
   if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
+  const int64_t n = (int64_t)L->last_T * L->last_K;
+  if (capacity < n)
+    return fail(HY3X_E_ARG, "routing buffers hold %lld entries, the last forward has %d x %d",
+                (long long)capacity, L->last_T, L->last_K);
   HIP_TRY(hipStreamSynchronize(L->last_stream));
-  const size_t n = (size_t)L->last_T * L->last_K;
   if (ids) HIP_TRY(hipMemcpy(ids, L->ids, n * sizeof(int32_t), hipMemcpyDeviceToHost));
   if (wpre) HIP_TRY(hipMemcpy(wpre, L->wpre, n * sizeof(float), hipMemcpyDeviceToHost));
   if (w) HIP_TRY(hipMemcpy(w, L->w, n * sizeof(float), hipMemcpyDeviceToHost));
@@ -603,27 +635,29 @@ int hy3x_diag_read_rate(const void *pool, int64_t pool_bytes, int64_t bytes, int
   if (!pool || !us || bytes < 16 || bytes % 16 || pool_bytes < bytes || reps < 1)
     return fail(HY3X_E_ARG, "bad read-rate arguments");
   hipStream_t st = (hipStream_t)stream;
-  uint32_t *sink = nullptr;
-  HIP_TRY(hipMalloc(&sink, 64));
+  struct Sink {
+    uint32_t *p = nullptr;
+    ~Sink() {
+      if (p) (void)hipFree(p);
+    }
+  } sink;
+  HIP_TRY(hipMalloc(&sink.p, 64));
   const int64_t slots = pool_bytes / bytes, n16 = bytes / 16;
   const unsigned grid = 2048;
   auto launch = [&](int i) {
     const uint4 *p = (const uint4 *)((const uint8_t *)pool + (i % slots) * bytes);
-    k_stream_read<<<grid, 256, 0, st>>>(p, n16, sink);
+    k_stream_read<<<grid, 256, 0, st>>>(p, n16, sink.p);
   };
   for (int i = 0; i < 10; i++) launch(i);
-  hipEvent_t e0, e1;
-  HIP_TRY(hipEventCreate(&e0));
-  HIP_TRY(hipEventCreate(&e1));
-  HIP_TRY(hipEventRecord(e0, st));
+  EventPair ev;
+  HIP_TRY(ev.create());
+  HIP_TRY(hipEventRecord(ev.a, st));
   for (int i = 0; i < reps; i++) launch(i);
-  HIP_TRY(hipEventRecord(e1, st));
-  HIP_TRY(hipEventSynchronize(e1));
+  HIP_TRY(hipEventRecord(ev.b, st));
+  HIP_TRY(hipEventSynchronize(ev.b));
   float ms = 0.0f;
-  HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  (void)hipFree(sink);
+  HIP_TRY(hipEventElapsedTime(&ms, ev.a, ev.b));
+  HIP_TRY(hipGetLastError());
   *us = ms * 1e3f / reps;
   return HY3X_OK;
 }

@@ -68,10 +68,7 @@ constexpr int RB_CHUNKS = 9;    // 16-byte chunks per row-block (144 B)
 constexpr int A_CHUNKS = RB * RB_CHUNKS;              // 2304 per column
 constexpr int A_CHUNKS_WAVE = A_CHUNKS / MT_WAVES;    // 288 per wave (32 row-blocks)
 constexpr int A_DMA = (A_CHUNKS_WAVE + 63) / 64;      // 5 copies per wave (last one half)
-#ifndef HY3X_A_STAGES
-#define HY3X_A_STAGES 2
-#endif
-constexpr int A_STAGES = HY3X_A_STAGES;               // weight ring stages
+constexpr int A_STAGES = 2;                           // weight ring stages
 constexpr int A_AHEAD = A_STAGES - 1;                 // weight columns copied ahead
 constexpr int B_DMA = MT_TOK * 32 / 64 / MT_WAVES;    // activation copies per wave
 constexpr int S_LANES = MT_TOK * 4 / MT_WAVES;        // lanes per wave copying sums
@@ -89,14 +86,10 @@ __shared__ __attribute__((aligned(16))) u4_t bt_st[2][MT_TOK][32];
 __shared__ __attribute__((aligned(16))) u4_t bm_st[2][MT_TOK][4];
 __shared__ int32_t t_slot[MT_TOK], t_arow[MT_TOK];
 
-// dma16_stream is the weight copy (dma16 with an optional cache policy):
-// HY3X_WEIGHT_POLICY can add a policy suffix to it (the default caching
-// measured best: a non-temporal " nt" was ~15% slower).
-#ifndef HY3X_WEIGHT_POLICY
-#define HY3X_WEIGHT_POLICY ""
-#endif
+// dma16_stream is the weight copy, with the default cache policy (a
+// non-temporal one measured ~15% slower).
 __device__ __forceinline__ void dma16_stream(const void *sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" HY3X_WEIGHT_POLICY ::"v"(voff), "s"(sbase),
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
                "{m0}"(lds)
                : "memory");
 }

@@ -76,7 +76,7 @@ __device__ __forceinline__ void router_block(
     const float *__restrict__ norm_w, const float *__restrict__ router,
     const float *__restrict__ bias, int has_bias, float *__restrict__ logits,
     float *__restrict__ sig, float *__restrict__ score, __half *__restrict__ s16,
-    float *__restrict__ s32, unsigned long long *trace) {
+    float *__restrict__ s32, unsigned long long *trace, const float *__restrict__ r_in) {
   __shared__ __attribute__((aligned(16))) float xsf[8 * RS], wsf[8 * RS], rsf[8 * RS];
   const int tid = threadIdx.x;
   trace_point(trace, 0);
@@ -104,7 +104,7 @@ __device__ __forceinline__ void router_block(
     }
     __shared__ float red_l[4];
     const float ss = block_sumsq(a, red_l);  // contains the barrier for the LDS rows
-    r_blk = 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
+    r_blk = r_in ? r_in[t] : 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
   }
   trace_point(trace, 1);
   const float r = r_blk;
@@ -133,10 +133,10 @@ __global__ __launch_bounds__(256) void k_router_logits(
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
     __half *__restrict__ s16, float *__restrict__ s32, unsigned long long *trace, int T,
-    uint32_t *__restrict__ bits, int wt) {
+    uint32_t *__restrict__ bits, int wt, const float *__restrict__ r_in) {
   if (bits) dispatch_clear_part(T, bits, wt, blockIdx.y * E + blockIdx.x, E * T);
   router_block(blockIdx.x, blockIdx.y, x, xadd, norm_w, router, bias, has_bias, logits, sig,
-               score, s16, s32, trace);
+               score, s16, s32, trace, r_in);
 }
 
 // Single token: router logits and the shared expert's gate/up in one launch.
@@ -154,11 +154,12 @@ __global__ __launch_bounds__(256) void k_route_decode(
     const float *__restrict__ router, const float *__restrict__ bias, int has_bias, int K,
     float *__restrict__ logits, float *__restrict__ sig, float *__restrict__ score,
     __half *__restrict__ s16, float *__restrict__ s32, const uint8_t *__restrict__ wq,
-    const uint8_t *__restrict__ wsh, __half *__restrict__ h16, unsigned long long *trace) {
+    const uint8_t *__restrict__ wsh, __half *__restrict__ h16, unsigned long long *trace,
+    const float *__restrict__ r_in) {
   const int tid = threadIdx.x;
   if (blockIdx.x < E) {
     router_block(blockIdx.x, 0, x, xadd, norm_w, router, bias, has_bias, logits, sig, score, s16,
-                 s32, trace);
+                 s32, trace, r_in);
     return;
   }
   // shared expert: s = rmsnorm(x) * norm_w, pair-staged fp16 in LDS. The
@@ -184,7 +185,8 @@ __global__ __launch_bounds__(256) void k_route_decode(
         a[u] = make_float4(a[u].x + ad[u].x, a[u].y + ad[u].y, a[u].z + ad[u].z,
                            a[u].w + ad[u].w);
     }
-    const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
+    const float ss = block_sumsq(a, red_l);
+    const float r = r_in ? r_in[0] : 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int j = 4 * (tid + 256 * u);
@@ -223,7 +225,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
                                                  float *__restrict__ s32,
                                                  __half *__restrict__ s16m,
                                                  __half *__restrict__ ssum, int T,
-                                                 uint32_t *__restrict__ bits, int wt) {
+                                                 uint32_t *__restrict__ bits, int wt,
+                                                 const float *__restrict__ r_in) {
   const int t = blockIdx.x, tid = threadIdx.x;
   if (bits) dispatch_clear_part(T, bits, wt, t, T);
   const float *xt = x + (size_t)t * D, *at = xadd ? xadd + (size_t)t * D : nullptr;
@@ -232,7 +235,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
 #pragma unroll
   for (int u = 0; u < 4; u++) a[u] = load_x4(xt, at, tid + 256 * u);
   __shared__ float red_l[4];
-  const float r = 1.0f / __builtin_sqrtf(block_sumsq(a, red_l) / 4096.0f + 1e-5f);
+  const float ss = block_sumsq(a, red_l);
+  const float r = r_in ? r_in[t] : 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
 #pragma unroll
   for (int u = 0; u < 4; u++) {
     const float4 w = wg[tid + 256 * u];

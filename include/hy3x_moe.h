@@ -140,10 +140,16 @@ int hy3x_layer_forward(hy3x_layer *layer, float *x, int T, int K, float scale, v
 int hy3x_layer_forward_residual(hy3x_layer *layer, float *x, const float *attn_out, int T, int K,
                                 float scale, void *stream);
 
+/* Token and expert counts (T, K) of the last forward. */
+int hy3x_layer_last_shape(const hy3x_layer *layer, int *T, int *K);
+
 /* Routing of the last forward, copied to host buffers (synchronises on the
  * stream): ids[T x K] int32 in selection order, wpre[T x K] = sigma / sum
- * (before the scale), w[T x K] (after). Any pointer may be NULL. */
-int hy3x_layer_last_routing(hy3x_layer *layer, int32_t *ids, float *wpre, float *w);
+ * (before the scale), w[T x K] (after). Any pointer may be NULL. capacity:
+ * the number of entries each non-NULL buffer holds; HY3X_E_ARG if it is
+ * below T x K of the last forward (nothing is copied then). */
+int hy3x_layer_last_routing(hy3x_layer *layer, int32_t *ids, float *wpre, float *w,
+                            int64_t capacity);
 
 /* Per-stage timing (diagnostics, no counterpart in the reference beyond its
  * HY3_TIMING wall clocks, hy3.c:1532-1563): while enabled, every forward
@@ -187,6 +193,15 @@ int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_to
  * 1 gate/up, 2 down). buf: device memory of 8 x 64-bit words per block, or
  * NULL to stop. Each block writes REALTIME-counter (100 MHz) checkpoints. */
 int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
+
+/* Diagnostics: substitute the RMSNorm scale. From this call on, a forward of
+ * T <= n tokens uses r[t] (host array of n floats, copied) as token t's
+ * 1/sqrt(mean(x^2) + 1e-5) instead of computing it; s = (x * norm_w) * r[t]
+ * as before. n = 0 switches back to the computed scale. No reference
+ * counterpart: it lets a test feed the reference CPU build's own r (from the
+ * host's rsqrt estimate and a Newton step, hy3.c:435-444 as compiled) and
+ * compare the rest of the routing to it. */
+int hy3x_layer_set_rms_scale(hy3x_layer *layer, const float *r, int n);
 
 /* Execution-path override for tests: 0 = automatic (by T), 1 = force the
  * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path (tile
