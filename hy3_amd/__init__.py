@@ -58,6 +58,7 @@ _SIGS = {
     "hy3x_synth_quantize_q8_0": (I32, [P, P, I64, P]),
     "hy3x_layer_forward": (I32, [P, P, I32, I32, F32, P]),
     "hy3x_layer_forward_residual": (I32, [P, P, P, I32, I32, F32, P]),
+    "hy3x_layer_forward_static": (I32, [P, P, I32, I32, F32, P]),
     "hy3x_layer_last_routing": (I32, [P, P, P, P, I64]),
     "hy3x_layer_last_shape": (I32, [P, ctypes.POINTER(I32), ctypes.POINTER(I32)]),
     "hy3x_layer_set_path": (I32, [P, I32]),
@@ -259,6 +260,11 @@ class MoELayer:
     def forward(self, x_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE, stream=None):
         """In-place MoE block on device memory x[T x 4096] (fp32)."""
         _check(lib().hy3x_layer_forward(self._h, x_dev_ptr, T, K, scale, stream))
+
+    def forward_static(self, x_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE, stream=None):
+        """forward() on the library's static per-GPU scratch: no allocation
+        (hy3x_layer_forward_static; T <= 64)."""
+        _check(lib().hy3x_layer_forward_static(self._h, x_dev_ptr, T, K, scale, stream))
 
     def forward_residual(self, x_dev_ptr, attn_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE,
                          stream=None):

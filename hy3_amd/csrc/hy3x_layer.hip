@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -26,6 +27,24 @@ using namespace hy3x;
 // dispatch tiles, or GEMV over dispatch tiles.
 enum class Mode { DECODE, MFMA, GEMV };
 
+// Per-forward device scratch for up to max_tokens tokens: routing (logits,
+// sigmoid, scores, ids, weights), the staged activations s and h in the
+// layouts their kernels read, the expert output rows and the dispatch lists.
+// One allocation (or the library's static array, hy3x_layer_forward_static),
+// carved by scratch_layout.
+struct Scratch {
+  int max_tokens = 0;
+  int wt = 0;         // bitmap words per expert (max_tokens / 32, rounded up to 4)
+  int max_tiles = 0;  // dispatch tiles the tile array holds
+  float *logits = nullptr, *sig = nullptr, *score = nullptr, *wpre = nullptr, *w = nullptr;
+  float *out = nullptr, *s32 = nullptr;
+  __half *s16 = nullptr, *h16 = nullptr, *s16m = nullptr, *h16m = nullptr;
+  __half *ssum = nullptr, *hsum = nullptr;  // sub-block sums (hi, lo) of s16m / h16m rows
+  int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
+  int4 *tiles = nullptr;
+  uint32_t *bits = nullptr;  // dispatch: per-expert token bitmaps [E][wt]
+};
+
 struct hy3x_layer {
   int device = 0;
   int max_tokens = 0;
@@ -34,18 +53,11 @@ struct hy3x_layer {
   int shared_q8 = 0;           // 1: the forward uses wsh for the shared expert
   float *norm_w = nullptr, *router = nullptr, *bias = nullptr;
   int has_bias = 0, router_set = 0;
-  float *logits = nullptr, *sig = nullptr, *score = nullptr, *wpre = nullptr, *w = nullptr, *out = nullptr;
-  __half *s16 = nullptr, *h16 = nullptr, *s16m = nullptr, *h16m = nullptr;
-  __half *ssum = nullptr, *hsum = nullptr;  // sub-block sums (hi, lo) of s16m / h16m rows
-  float *s32 = nullptr;
-  int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
-  int4 *tiles = nullptr;
-  uint32_t *bits = nullptr;    // dispatch: per-expert token bitmaps [E][wt]
-  int wt = 0;                  // bitmap words per expert (max_tokens / 32, rounded up to 4)
+  uint8_t *scratch_mem = nullptr;  // the layer's own scratch allocation
+  Scratch own;                 // carved from scratch_mem
   unsigned long long *stats = nullptr;
   float *rms_r = nullptr;      // diagnostics: RMSNorm scales substituted per token
   int rms_n = 0;               // tokens rms_r covers (0: compute r)
-  int max_tiles_alloc = 0;
   int last_T = 0, last_K = 0;
   struct Forward {  // launch parameters of the current / last forward
     float *x = nullptr;
@@ -55,6 +67,7 @@ struct hy3x_layer {
     Mode mode = Mode::GEMV;
     bool wide = false;  // MFMA mode: the wide tile shape (mfma_wide)
     const float *r_in = nullptr;  // substituted RMSNorm scales, or null
+    Scratch sc;         // the scratch this forward runs on
   } cur;
   hipStream_t last_stream = nullptr;
   int path = 0;
@@ -152,9 +165,108 @@ constexpr int kMfmaMinT = 2;
 // mostly empty and one workgroup per CU hides less latency than two.
 constexpr int kMfmaWideMinT = 384;
 
-static int max_tiles_for(int T, int K, int NT) {
+static constexpr int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
   return n / NT + std::min(E, n) + (T + NT - 1) / NT + 1;
+}
+
+// The pieces of a forward's scratch, in carving order, and their bytes for
+// max_tokens tokens (slots = tokens x (K_MAX routed + 1 shared)).
+enum ScratchPiece {
+  SP_LOGITS, SP_SIG, SP_SCORE, SP_WPRE, SP_W, SP_IDS, SP_S16, SP_S32, SP_S16M, SP_H16M,
+  SP_SSUM, SP_HSUM, SP_H16, SP_OUT, SP_LIST, SP_TILES, SP_NTILES, SP_COUNTS, SP_BITS, SP_COUNT
+};
+constexpr int bitmap_words(int max_tokens) { return ((max_tokens + 31) / 32 + 3) & ~3; }
+constexpr size_t piece_bytes(int max_tokens, int piece) {
+  const size_t T = (size_t)max_tokens, slots = T * (KMAX + 1);
+  switch (piece) {
+    case SP_LOGITS: case SP_SIG: case SP_SCORE: return T * E * sizeof(float);
+    case SP_WPRE: case SP_W: return T * KMAX * sizeof(float);
+    case SP_IDS: return T * KMAX * sizeof(int32_t);
+    case SP_S16: case SP_S16M: return T * D * sizeof(__half);
+    case SP_S32: return T * D * sizeof(float);
+    case SP_H16M: case SP_H16: return slots * F * sizeof(__half);
+    case SP_SSUM: return T * (D / 32) * 4 * sizeof(__half);
+    case SP_HSUM: return slots * (F / 32) * 4 * sizeof(__half);
+    case SP_OUT: return slots * D * sizeof(float);
+    case SP_LIST: return slots * sizeof(int32_t);
+    case SP_TILES: return (size_t)max_tiles_for(max_tokens, KMAX, 1) * sizeof(int4);
+    case SP_NTILES: return sizeof(int32_t);
+    case SP_COUNTS: return (E + 1) * sizeof(int32_t);
+    case SP_BITS: return (size_t)E * bitmap_words(max_tokens) * sizeof(uint32_t);
+  }
+  return 0;
+}
+constexpr size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+constexpr size_t scratch_bytes(int max_tokens) {
+  size_t off = 0;
+  for (int i = 0; i < SP_COUNT; i++) off += align256(piece_bytes(max_tokens, i));
+  return off;
+}
+
+// Carves the scratch of max_tokens tokens out of base (scratch_bytes(max_tokens)
+// bytes, 256-byte aligned; every piece 256-byte aligned).
+static Scratch scratch_layout(int max_tokens, uint8_t *base) {
+  Scratch S;
+  void *p[SP_COUNT];
+  size_t off = 0;
+  for (int i = 0; i < SP_COUNT; i++) {
+    p[i] = base + off;
+    off += align256(piece_bytes(max_tokens, i));
+  }
+  S.logits = (float *)p[SP_LOGITS];
+  S.sig = (float *)p[SP_SIG];
+  S.score = (float *)p[SP_SCORE];
+  S.wpre = (float *)p[SP_WPRE];
+  S.w = (float *)p[SP_W];
+  S.ids = (int32_t *)p[SP_IDS];
+  S.s16 = (__half *)p[SP_S16];
+  S.s32 = (float *)p[SP_S32];
+  S.s16m = (__half *)p[SP_S16M];
+  S.h16m = (__half *)p[SP_H16M];
+  S.ssum = (__half *)p[SP_SSUM];
+  S.hsum = (__half *)p[SP_HSUM];
+  S.h16 = (__half *)p[SP_H16];
+  S.out = (float *)p[SP_OUT];
+  S.list = (int32_t *)p[SP_LIST];
+  S.tiles = (int4 *)p[SP_TILES];
+  S.n_tiles = (int32_t *)p[SP_NTILES];
+  S.counts = (int32_t *)p[SP_COUNTS];
+  S.bits = (uint32_t *)p[SP_BITS];
+  S.max_tokens = max_tokens;
+  S.wt = bitmap_words(max_tokens);
+  S.max_tiles = max_tiles_for(max_tokens, KMAX, 1);
+  return S;
+}
+
+// The no-allocation entry point's scratch: one array per GPU, sized for
+// HY3X_STATIC_MAX_TOKENS tokens, held by every GPU the library runs on until
+// the process ends. Host code never passes `scratch` itself to a kernel (on
+// the host it names a stand-in, not device memory): static_scratch_ptr()
+// looks up this device's copy once with hipGetSymbolAddress and every use
+// goes through that address.
+constexpr size_t kStaticScratchBytes = scratch_bytes(HY3X_STATIC_MAX_TOKENS);
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_static_mu;
+static uint8_t *g_static_ptr[kMaxDevices];
+
+// This device's address of `scratch` (looked up on the device's first call).
+static int static_scratch_ptr(int device, uint8_t **out) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(HY3X_E_ARG, "device %d outside [0,%d)", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (!g_static_ptr[device]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(HY3X_E_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                  hipGetErrorString(e));
+    g_static_ptr[device] = (uint8_t *)ptr;
+  }
+  *out = g_static_ptr[device];
+  return HY3X_OK;
 }
 
 extern "C" {
@@ -168,9 +280,7 @@ int hy3x_set_device(int device) {
 
 int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
-  void *ptrs[] = {L->wq, L->wsh, L->sig, L->score,  L->norm_w, L->router, L->bias,    L->logits,  L->wpre,
-                  L->w,    L->out,    L->s16, L->s32, L->s16m, L->h16m, L->ssum, L->hsum, L->h16,     L->ids,     L->list,
-                  L->n_tiles, L->counts, L->tiles, L->bits, L->stats, L->rms_r};
+  void *ptrs[] = {L->wq, L->wsh, L->norm_w, L->router, L->bias, L->scratch_mem, L->stats, L->rms_r};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   for (hipEvent_t ev : L->ev_pool) (void)hipEventDestroy(ev);
@@ -189,39 +299,18 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
     return fail(HY3X_E_HIP, "hipGetDevice failed");
   }
   L->max_tokens = max_tokens;
-  const size_t T = (size_t)max_tokens, slots = T * (KMAX + 1);
-  L->max_tiles_alloc = max_tiles_for(max_tokens, KMAX, 1);
-  L->wt = ((max_tokens + 31) / 32 + 3) & ~3;  // 16-byte rows
   int rc = HY3X_OK;
   if ((rc = dalloc(&L->wq, (size_t)(E + 1) * EXPERT_BYTES)) ||
       (rc = dalloc(&L->norm_w, D * sizeof(float))) ||
       (rc = dalloc(&L->router, (size_t)E * D * sizeof(float))) ||
       (rc = dalloc(&L->bias, E * sizeof(float))) ||
-      (rc = dalloc(&L->logits, T * E * sizeof(float))) ||
-      (rc = dalloc(&L->sig, T * E * sizeof(float))) ||
-      (rc = dalloc(&L->score, T * E * sizeof(float))) ||
-      (rc = dalloc(&L->wpre, T * KMAX * sizeof(float))) ||
-      (rc = dalloc(&L->w, T * KMAX * sizeof(float))) ||
-      (rc = dalloc(&L->ids, T * KMAX * sizeof(int32_t))) ||
-      (rc = dalloc(&L->s16, T * D * sizeof(__half))) ||
-      (rc = dalloc(&L->s32, T * D * sizeof(float))) ||
-      (rc = dalloc(&L->s16m, T * D * sizeof(__half))) ||
-      (rc = dalloc(&L->h16m, slots * F * sizeof(__half))) ||
-      (rc = dalloc(&L->ssum, T * (D / 32) * 4 * sizeof(__half))) ||
-      (rc = dalloc(&L->hsum, slots * (F / 32) * 4 * sizeof(__half))) ||
-      (rc = dalloc(&L->h16, slots * F * sizeof(__half))) ||
-      (rc = dalloc(&L->out, slots * D * sizeof(float))) ||
-      (rc = dalloc(&L->list, slots * sizeof(int32_t))) ||
-      (rc = dalloc(&L->tiles, (size_t)L->max_tiles_alloc * sizeof(int4))) ||
-      (rc = dalloc(&L->n_tiles, sizeof(int32_t))) ||
-      (rc = dalloc(&L->counts, (E + 1) * sizeof(int32_t))) ||
-      (rc = dalloc(&L->bits, (size_t)E * L->wt * sizeof(uint32_t))) ||
+      (rc = dalloc(&L->scratch_mem, scratch_bytes(max_tokens))) ||
       (rc = dalloc(&L->stats, 2 * sizeof(unsigned long long)))) {
     hy3x_layer_destroy(L);
     return rc;
   }
-  if (hipMemset(L->bits, 0, (size_t)E * L->wt * sizeof(uint32_t)) != hipSuccess ||
-      hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
+  L->own = scratch_layout(max_tokens, L->scratch_mem);
+  if (hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
       hipMemset(L->stats, 0, 2 * sizeof(unsigned long long)) != hipSuccess) {
     hy3x_layer_destroy(L);
     return fail(HY3X_E_HIP, "hipMemset failed");
@@ -336,112 +425,130 @@ int hy3x_layer_last_path(const hy3x_layer *L, int *path) {
 // forward and the kernel replay used for timing).
 static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
   const auto &c = L->cur;
+  const Scratch &S = c.sc;
   const int T = c.T, K = c.K, mt = c.mt;
   float *x = c.x;
   switch (stage) {
     case HY3X_STAGE_ROUTER:
       if (c.mode == Mode::DECODE) {
         k_route_decode<<<E + DEC_SH_BLOCKS, 256, 0, st>>>(
-            x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, L->logits, L->sig, L->score,
-            L->s16, L->s32, L->wq, L->shared_q8 ? L->wsh : nullptr, L->h16, L->trace[0], c.r_in);
+            x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, S.logits, S.sig, S.score,
+            S.s16, S.s32, L->wq, L->shared_q8 ? L->wsh : nullptr, S.h16, L->trace[0], c.r_in);
         break;
       }
       // the routing kernels also clear (first kernel) and fill (top-K) the
       // dispatch bitmaps; for T > 8 the RMSNorm kernel stages the MFMA operand
       if (T <= kSmallRouterT) {
         k_router_logits<<<dim3(E, T), 256, 0, st>>>(x, c.xadd, L->norm_w, L->router, L->bias,
-                                                    L->has_bias, L->logits, L->sig, L->score,
-                                                    L->s16, L->s32, L->trace[0], T, L->bits,
-                                                    L->wt, c.r_in);
+                                                    L->has_bias, S.logits, S.sig, S.score,
+                                                    S.s16, S.s32, L->trace[0], T, S.bits,
+                                                    S.wt, c.r_in);
       } else {
         const bool mf = c.mode == Mode::MFMA;
-        k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : L->s16, L->s32,
-                                     mf ? L->s16m : nullptr, L->ssum, T, L->bits, L->wt,
+        k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : S.s16, S.s32,
+                                     mf ? S.s16m : nullptr, S.ssum, T, S.bits, S.wt,
                                      c.r_in);
         if (T <= kTinyRouterT)
           k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
-              L->s32, L->router, T, L->logits);
+              S.s32, L->router, T, S.logits);
         else if (T <= kMidRouterT)
           k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
-              L->s32, L->router, T, L->logits);
+              S.s32, L->router, T, S.logits);
         else if (T <= kLargeRouterT)
           k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 15) / 16, E / 16), 256, 0, st>>>(
-              L->s32, L->router, T, L->logits);
+              S.s32, L->router, T, S.logits);
         else
           k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
-              L->s32, L->router, T, L->logits);
+              S.s32, L->router, T, S.logits);
       }
       {
         // one wave per token; up to 256 tokens one wave per block, so that
         // few tokens still spread over many CUs
         const int wpb = T <= 256 ? 1 : 4;
-        k_topk<<<(T + wpb - 1) / wpb, 64 * wpb, 0, st>>>(L->logits, L->bias, L->has_bias, K,
-                                                         c.scale, T, L->ids, L->wpre, L->w,
-                                                         L->bits, L->wt);
+        k_topk<<<(T + wpb - 1) / wpb, 64 * wpb, 0, st>>>(S.logits, L->bias, L->has_bias, K,
+                                                         c.scale, T, S.ids, S.wpre, S.w,
+                                                         S.bits, S.wt);
       }
       break;
     case HY3X_STAGE_DISPATCH:
       if (c.mode == Mode::MFMA && T <= kSmallRouterT)
-        k_stage_mfma<<<T, 256, 0, st>>>(L->s32, L->s16m, L->ssum);
+        k_stage_mfma<<<T, 256, 0, st>>>(S.s32, S.s16m, S.ssum);
       if (c.mode != Mode::DECODE) {
-        k_dispatch_list<<<E + 1, 256, 0, st>>>(L->ids, T, K, c.nt, L->bits, L->wt,
-                                               L->list, L->tiles, L->n_tiles, mt, L->counts,
+        k_dispatch_list<<<E + 1, 256, 0, st>>>(S.ids, T, K, c.nt, S.bits, S.wt,
+                                               S.list, S.tiles, S.n_tiles, mt, S.counts,
                                                L->stats);
       }
       break;
     case HY3X_STAGE_GATEUP:
       if (c.mode == Mode::DECODE)
-        k_gateup_decode<<<K * DEC_GU_BLOCKS, 64 * DEC_GU_WAVES, 0, st>>>(L->wq, L->s16, L->sig, L->score, K,
-                                                          c.scale, L->ids, L->wpre, L->w,
-                                                          L->stats, L->h16, L->trace[1]);
+        k_gateup_decode<<<K * DEC_GU_BLOCKS, 64 * DEC_GU_WAVES, 0, st>>>(L->wq, S.s16, S.sig, S.score, K,
+                                                          c.scale, S.ids, S.wpre, S.w,
+                                                          L->stats, S.h16, L->trace[1]);
       else if (c.mode == Mode::MFMA && c.wide)
         mfma_wide::k_moe_mfma<true>
             <<<mt * (F / mfma_wide::ROWS_GU), 64 * mfma_wide::WAVES, 0, st>>>(
-                L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list, L->tiles,
-                L->n_tiles, T, K, L->h16m, nullptr);
+                L->wq, L->shared_q8 ? L->wsh : nullptr, S.s16m, S.ssum, S.list, S.tiles,
+                S.n_tiles, T, K, S.h16m, nullptr);
       else if (c.mode == Mode::MFMA)
         mfma_narrow::k_moe_mfma<true>
             <<<mt * (F / mfma_narrow::ROWS_GU), 64 * mfma_narrow::WAVES, 0, st>>>(
-                L->wq, L->shared_q8 ? L->wsh : nullptr, L->s16m, L->ssum, L->list, L->tiles,
-                L->n_tiles, T, K, L->h16m, nullptr);
+                L->wq, L->shared_q8 ? L->wsh : nullptr, S.s16m, S.ssum, S.list, S.tiles,
+                S.n_tiles, T, K, S.h16m, nullptr);
       else
-        k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, L->s16, L->list, L->tiles,
-                                                        L->n_tiles, T, K, L->h16);
+        k_gateup_gemv<4><<<mt * (F / 16), 256, 0, st>>>(L->wq, S.s16, S.list, S.tiles,
+                                                        S.n_tiles, T, K, S.h16);
       break;
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
         k_down_decode<<<D / DEC_DOWN_RPB, 64 * (KMAX + 1), 0, st>>>(
-            L->wq, L->h16, L->ids, L->w, K, x, c.xadd, L->shared_q8 ? L->wsh : nullptr,
+            L->wq, S.h16, S.ids, S.w, K, x, c.xadd, L->shared_q8 ? L->wsh : nullptr,
             L->trace[2]);
       else if (c.mode == Mode::MFMA) {
-        k_hsums<<<T * (K + 1), 64, 0, st>>>(L->h16m, L->hsum);
+        k_hsums<<<T * (K + 1), 64, 0, st>>>(S.h16m, S.hsum);
         const uint8_t *wsh = L->shared_q8 ? L->wsh : nullptr;
         if (c.wide)
           mfma_wide::k_moe_mfma<false>
               <<<mt * (D / (2 * mfma_wide::ROWS_GU)), 64 * mfma_wide::WAVES, 0, st>>>(
-                  L->wq, wsh, L->h16m, L->hsum, L->list, L->tiles, L->n_tiles, T, K, nullptr,
-                  L->out);
+                  L->wq, wsh, S.h16m, S.hsum, S.list, S.tiles, S.n_tiles, T, K, nullptr,
+                  S.out);
         else
           mfma_narrow::k_moe_mfma<false>
               <<<mt * (D / (2 * mfma_narrow::ROWS_GU)), 64 * mfma_narrow::WAVES, 0, st>>>(
-                  L->wq, wsh, L->h16m, L->hsum, L->list, L->tiles, L->n_tiles, T, K, nullptr,
-                  L->out);
+                  L->wq, wsh, S.h16m, S.hsum, S.list, S.tiles, S.n_tiles, T, K, nullptr,
+                  S.out);
       }
       else
-        k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, L->h16, L->list, L->tiles,
-                                                      L->n_tiles, L->out);
+        k_down_gemv<4><<<mt * (D / 32), 256, 0, st>>>(L->wq, S.h16, S.list, S.tiles,
+                                                      S.n_tiles, S.out);
       break;
     case HY3X_STAGE_COMBINE:
-      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 1024, T), 256, 0, st>>>(x, c.xadd, L->out, L->w, T, K);
+      if (c.mode != Mode::DECODE) k_combine<<<dim3(D / 1024, T), 256, 0, st>>>(x, c.xadd, S.out, S.w, T, K);
       break;
   }
 }
 
-static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K, float scale,
-                        void *stream);
+static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float *xadd, int T,
+                        int K, float scale, void *stream);
 
 int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
-  return forward_impl(L, x, nullptr, T, K, scale, stream);
+  return forward_impl(L, L ? &L->own : nullptr, x, nullptr, T, K, scale, stream);
+}
+
+int hy3x_layer_forward_static(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
+  if (!L) return fail(HY3X_E_ARG, "NULL layer");
+  if (T < 1 || T > HY3X_STATIC_MAX_TOKENS)
+    return fail(HY3X_E_ARG, "T=%d outside [1,%d] (the static scratch's maximum)", T,
+                HY3X_STATIC_MAX_TOKENS);
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev != L->device)
+    return fail(HY3X_E_ARG, "the layer lives on device %d, the current device is %d", L->device,
+                dev);
+  uint8_t *base = nullptr;
+  const int rc = static_scratch_ptr(dev, &base);
+  if (rc) return rc;
+  const Scratch sc = scratch_layout(HY3X_STATIC_MAX_TOKENS, base);
+  return forward_impl(L, &sc, x, nullptr, T, K, scale, stream);
 }
 
 int hy3x_layer_forward_residual(hy3x_layer *L, float *x, const float *attn_out, int T, int K,
@@ -453,13 +560,14 @@ int hy3x_layer_forward_residual(hy3x_layer *L, float *x, const float *attn_out, 
     const uintptr_t n = (uintptr_t)T * D * sizeof(float);
     if (a0 < b0 + n && b0 < a0 + n) return fail(HY3X_E_ARG, "attn_out overlaps x");
   }
-  return forward_impl(L, x, attn_out, T, K, scale, stream);
+  return forward_impl(L, L ? &L->own : nullptr, x, attn_out, T, K, scale, stream);
 }
 
-static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K, float scale,
-                        void *stream) {
-  if (!L || !x) return fail(HY3X_E_ARG, "NULL argument");
-  if (T < 1 || T > L->max_tokens) return fail(HY3X_E_ARG, "T=%d outside [1,%d]", T, L->max_tokens);
+static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float *xadd, int T,
+                        int K, float scale, void *stream) {
+  if (!L || !x || !sc) return fail(HY3X_E_ARG, "NULL argument");
+  if (T < 1 || T > sc->max_tokens)
+    return fail(HY3X_E_ARG, "T=%d outside [1,%d]", T, sc->max_tokens);
   if (K < 1 || K > KMAX) return fail(HY3X_E_ARG, "K=%d outside [1,8]", K);
   if (!L->router_set) return fail(HY3X_E_STATE, "router not set");
   hipStream_t st = (hipStream_t)stream;
@@ -469,6 +577,7 @@ static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K
   c.T = T;
   c.K = K;
   c.scale = scale;
+  c.sc = *sc;
   c.r_in = L->rms_n >= T ? L->rms_r : nullptr;
   if (T == 1 && L->path == 0)
     c.mode = Mode::DECODE;
@@ -482,7 +591,7 @@ static int forward_impl(hy3x_layer *L, float *x, const float *xadd, int T, int K
            (L->path == 4 || (L->path != 3 && T >= kMfmaWideMinT));
   // tokens per work tile
   c.nt = c.mode != Mode::MFMA ? 4 : c.wide ? mfma_wide::TOKENS : mfma_narrow::TOKENS;
-  c.mt = std::min(max_tiles_for(T, K, c.nt), L->max_tiles_alloc);
+  c.mt = std::min(max_tiles_for(T, K, c.nt), sc->max_tiles);
   record_stage(L, st, -1);
   for (int stage = HY3X_STAGE_ROUTER; stage <= HY3X_STAGE_COMBINE; stage++) {
     if (c.mode == Mode::DECODE && (stage == HY3X_STAGE_DISPATCH || stage == HY3X_STAGE_COMBINE))
@@ -576,9 +685,10 @@ int hy3x_layer_last_routing(hy3x_layer *L, int32_t *ids, float *wpre, float *w,
     return fail(HY3X_E_ARG, "routing buffers hold %lld entries, the last forward has %d x %d",
                 (long long)capacity, L->last_T, L->last_K);
   HIP_TRY(hipStreamSynchronize(L->last_stream));
-  if (ids) HIP_TRY(hipMemcpy(ids, L->ids, n * sizeof(int32_t), hipMemcpyDeviceToHost));
-  if (wpre) HIP_TRY(hipMemcpy(wpre, L->wpre, n * sizeof(float), hipMemcpyDeviceToHost));
-  if (w) HIP_TRY(hipMemcpy(w, L->w, n * sizeof(float), hipMemcpyDeviceToHost));
+  const Scratch &S = L->cur.sc;
+  if (ids) HIP_TRY(hipMemcpy(ids, S.ids, n * sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (wpre) HIP_TRY(hipMemcpy(wpre, S.wpre, n * sizeof(float), hipMemcpyDeviceToHost));
+  if (w) HIP_TRY(hipMemcpy(w, S.w, n * sizeof(float), hipMemcpyDeviceToHost));
   return HY3X_OK;
 }
 

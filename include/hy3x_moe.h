@@ -128,6 +128,24 @@ int hy3x_layer_expert_ptr(hy3x_layer *layer, int expert, int matrix, void **ptr)
  * the reference's ctx singleton buffers (hy3_gpu.cu:483, 616-621). */
 int hy3x_layer_forward(hy3x_layer *layer, float *x, int T, int K, float scale, void *stream);
 
+/* The largest T hy3x_layer_forward_static accepts. */
+#define HY3X_STATIC_MAX_TOKENS 64
+
+/* hy3x_layer_forward without any allocation at all, for callers that cannot
+ * call hipMalloc (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it). No counterpart in the reference. The forward's
+ * scratch (routing, staged activations, expert outputs, dispatch lists; about
+ * 15 MB) lives in one static device array per GPU instead of the layer's own
+ * buffers; each GPU the library runs on holds it until the process ends.
+ * 1 <= T <= HY3X_STATIC_MAX_TOKENS (HY3X_E_ARG beyond), K and scale as
+ * hy3x_layer_forward, same result bit for bit. Call it with the layer's
+ * device current. Every call on one GPU shares that GPU's array, whatever the
+ * layer: calls that overlap on one GPU (other streams, other threads) race,
+ * and hy3x_layer_last_routing reads the array as the last static call left
+ * it. Calls no hipMalloc, hipFree or allocating library routine. */
+int hy3x_layer_forward_static(hy3x_layer *layer, float *x, int T, int K, float scale,
+                              void *stream);
+
 /* The residual add before the block fused into it: x += attn_out, then the
  * MoE block on the new x, i.e. hy3.c:1264-1266 (x[i] += s2[i]; rms_norm...)
  * and the GPU engine's add_rmsnorm_kernel + gpu_ffn_moe (hy3_gpu.cu:453-460,
