@@ -48,6 +48,7 @@ _SIGS = {
     "hy3x_set_device": (I32, [I32]),
     "hy3x_layer_create": (I32, [ctypes.POINTER(P), I32]),
     "hy3x_layer_destroy": (I32, [P]),
+    "hy3x_layer_create_shared": (I32, [ctypes.POINTER(P), P]),
     "hy3x_layer_set_router": (I32, [P, P, P, P]),
     "hy3x_layer_set_expert_q4k": (I32, [P, I32, P, P, P, I32]),
     "hy3x_layer_expert_ptr": (I32, [P, I32, I32, ctypes.POINTER(P)]),

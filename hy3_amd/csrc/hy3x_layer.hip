@@ -45,6 +45,14 @@ struct Scratch {
   uint32_t *bits = nullptr;  // dispatch: per-expert token bitmaps [E][wt]
 };
 
+// A scratch allocation and the number of layers using it.
+struct ScratchMem {
+  uint8_t *mem = nullptr;
+  int max_tokens = 0;
+  int refs = 1;
+};
+static std::mutex g_scratch_mu;
+
 struct hy3x_layer {
   int device = 0;
   int max_tokens = 0;
@@ -53,7 +61,8 @@ struct hy3x_layer {
   int shared_q8 = 0;           // 1: the forward uses wsh for the shared expert
   float *norm_w = nullptr, *router = nullptr, *bias = nullptr;
   int has_bias = 0, router_set = 0;
-  uint8_t *scratch_mem = nullptr;  // the layer's own scratch allocation
+  ScratchMem *scratch_mem = nullptr;  // the scratch allocation (shared by layers made
+                                      // with hy3x_layer_create_shared)
   Scratch own;                 // carved from scratch_mem
   unsigned long long *stats = nullptr;
   float *rms_r = nullptr;      // diagnostics: RMSNorm scales substituted per token
@@ -278,17 +287,33 @@ int hy3x_set_device(int device) {
   return HY3X_OK;
 }
 
+static void release_scratch(ScratchMem *m) {
+  if (!m) return;
+  int left;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    left = --m->refs;
+  }
+  if (left == 0) {
+    if (m->mem) (void)hipFree(m->mem);
+    delete m;
+  }
+}
+
 int hy3x_layer_destroy(hy3x_layer *L) {
   if (!L) return HY3X_OK;
-  void *ptrs[] = {L->wq, L->wsh, L->norm_w, L->router, L->bias, L->scratch_mem, L->stats, L->rms_r};
+  void *ptrs[] = {L->wq, L->wsh, L->norm_w, L->router, L->bias, L->stats, L->rms_r};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
+  release_scratch(L->scratch_mem);
   for (hipEvent_t ev : L->ev_pool) (void)hipEventDestroy(ev);
   delete L;
   return HY3X_OK;
 }
 
-int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
+// A layer with its weights and counters; its scratch is `share`'s (one more
+// user) or, with share == null, a new allocation for max_tokens tokens.
+static int create_layer(hy3x_layer **out, int max_tokens, ScratchMem *share) {
   if (!out) return fail(HY3X_E_ARG, "out is NULL");
   *out = nullptr;
   if (max_tokens < 1 || max_tokens > (1 << 16))
@@ -299,17 +324,25 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
     return fail(HY3X_E_HIP, "hipGetDevice failed");
   }
   L->max_tokens = max_tokens;
+  if (share) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    share->refs++;
+    L->scratch_mem = share;
+  } else {
+    L->scratch_mem = new ScratchMem();
+    L->scratch_mem->max_tokens = max_tokens;
+  }
   int rc = HY3X_OK;
   if ((rc = dalloc(&L->wq, (size_t)(E + 1) * EXPERT_BYTES)) ||
       (rc = dalloc(&L->norm_w, D * sizeof(float))) ||
       (rc = dalloc(&L->router, (size_t)E * D * sizeof(float))) ||
       (rc = dalloc(&L->bias, E * sizeof(float))) ||
-      (rc = dalloc(&L->scratch_mem, scratch_bytes(max_tokens))) ||
+      (!share && (rc = dalloc(&L->scratch_mem->mem, scratch_bytes(max_tokens)))) ||
       (rc = dalloc(&L->stats, 2 * sizeof(unsigned long long)))) {
     hy3x_layer_destroy(L);
     return rc;
   }
-  L->own = scratch_layout(max_tokens, L->scratch_mem);
+  L->own = scratch_layout(max_tokens, L->scratch_mem->mem);
   if (hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
       hipMemset(L->stats, 0, 2 * sizeof(unsigned long long)) != hipSuccess) {
     hy3x_layer_destroy(L);
@@ -317,6 +350,20 @@ int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
   }
   *out = L;
   return HY3X_OK;
+}
+
+int hy3x_layer_create(hy3x_layer **out, int max_tokens) {
+  return create_layer(out, max_tokens, nullptr);
+}
+
+int hy3x_layer_create_shared(hy3x_layer **out, hy3x_layer *scratch_from) {
+  if (!scratch_from) return fail(HY3X_E_ARG, "scratch_from is NULL");
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev != scratch_from->device)
+    return fail(HY3X_E_ARG, "scratch_from lives on device %d, the current device is %d",
+                scratch_from->device, dev);
+  return create_layer(out, scratch_from->scratch_mem->max_tokens, scratch_from->scratch_mem);
 }
 
 int hy3x_layer_set_router(hy3x_layer *L, const float *norm_w, const float *router,

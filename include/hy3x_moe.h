@@ -67,6 +67,15 @@ int hy3x_set_device(int device);
 int hy3x_layer_create(hy3x_layer **out, int max_tokens);
 int hy3x_layer_destroy(hy3x_layer *layer);
 
+/* Another layer (own weights, router and counters) that shares the forward
+ * scratch of `scratch_from` (same max_tokens, same device; the allocation is
+ * freed with the last layer using it, in any destroy order). For an engine
+ * that runs its MoE layers one after another on one stream, as the
+ * reference's single set of MoE buffers (hy3_gpu.cu:616-621) serves all of
+ * hy3_gpu_init's layers: one scratch instead of one per layer. Forwards of
+ * layers sharing a scratch must not overlap. */
+int hy3x_layer_create_shared(hy3x_layer **out, hy3x_layer *scratch_from);
+
 /* Router-side tensors, host pointers, copied to the device:
  * norm_w[4096] (ffn_norm, F32), router[192 x 4096] (ffn_gate_inp, F32,
  * row-major as in GGUF), expert_bias[192] or NULL when the layer has no bias
