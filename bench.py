@@ -1,22 +1,30 @@
 """Benchmark: one Hy3 MoE FFN layer on one MI355X through libhy3x.so.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0..4]
-                    [--secondary] [--cpu-seconds S]
+                    [--rotate N] [--secondary] [--cpu-seconds S]
 
 A step is one forward of the MoE block (RMSNorm, router, top-8, 8 routed + 1
 shared Q4_K SwiGLU experts, combine, residual) over one batch of synthetic
-input already resident in HBM. The default workload is config 0 (decode, one
-token), the configuration of the north-star target; --secondary adds one line
-of results per other configuration inside the same JSON object.
+input already resident in HBM. The default line measures both halves of the
+headline metric: decode of one token (config 0; `value`) and one 512-token
+prefill chunk (config 2; the `prefill` object). The decode is timed cold:
+four distinct resident layers (8.2 GB of Q4_K) are cycled one per step, so
+no step finds its 99 MB of weights in the 256 MB last-level cache, as in a
+real 79-layer decode (--rotate 1 re-runs one layer, cache-warm).
+--secondary adds the other configurations inside the same JSON object.
 
 Prints ONE JSON line (rank 0). Fields beyond the driver's contract:
   roofline      dominant kernel: algorithmic bytes per launch / its mean launch
                 duration (HIP events on the launch stream around back-to-back
-                replays of that kernel after the timed steps); traffic = HBM bytes
-                per launch from the committed rocprofv3 PMC summary
-  cpu_baseline  the reference CPU MoE block (hy3.c forward_layer_moe built
-                from the reference sources, oracle/_ref) or, when that library
-                is absent, the oracle port, on a bounded token sample
+                launches of that kernel after the timed steps, rotating over the
+                same resident layers); traffic = HBM bytes per launch from the
+                committed rocprofv3 PMC summary
+  prefill       config 2 with its own roofline (HBM and MFMA fractions)
+  cpu_baseline  the reference CPU MoE block (hy3.c forward_layer_moe compiled
+                from the reference sources into oracle/_ref/libhy3ref.so, built
+                in the development container and shipped with the tree) or, when
+                that library is absent, the oracle port, on a bounded token
+                sample, with the host CPU model and the threads used
 """
 import argparse
 import dataclasses
@@ -44,6 +52,12 @@ def parse():
     p.add_argument("--config", type=int, default=0)
     p.add_argument("--secondary", action="store_true", help="also measure the other configs")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--rotate", type=int, default=4,
+                   help="distinct resident layers a one-layer config cycles through, one per "
+                        "step (4 x 2.05 GB: every step streams from HBM; 1: one layer re-run, "
+                        "cache-warm at decode)")
+    p.add_argument("--no-prefill", action="store_true",
+                   help="skip the 512-token prefill entry (config 2) of the default line")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--path", type=int, default=0, choices=(0, 1, 2, 3, 4),
                    help="expert path: 0 the library's choice by T, 1 GEMV tiles, 2 MFMA tiles, "
@@ -137,10 +151,18 @@ def dominant_kernel(stage, last_path):
 
 
 def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=False,
-            residual=False):
+            residual=False, rotate=1):
+    """Time `steps` forwards of cfg. A stacked config (n_layers > 1) runs all its
+    layers per step. A one-layer config with rotate > 1 keeps `rotate` distinct
+    layers of the same distribution resident (layer indices 0 .. rotate-1, one
+    shared scratch) and step i runs layer i % rotate: with their weights far
+    beyond the 256 MB last-level cache every step streams from HBM, as the
+    layers of a real decode do (cold timing). rotate = 1 re-runs one layer
+    (warm for a decode, whose 99 MB stay in the cache)."""
+    n_inst = cfg.n_layers if cfg.n_layers > 1 else rotate
     layers = []
-    for li in range(cfg.n_layers):
-        L = H.MoELayer(cfg.T)
+    for li in range(n_inst):
+        L = H.MoELayer(cfg.T, share_scratch_with=layers[0] if layers else None)
         L.synth_experts(cfg.weight_seed, li)
         if shared_q8:
             L.synth_shared_q8_0(cfg.weight_seed, li)
@@ -153,17 +175,27 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
     # residual addend (attention output stand-in): a small multiple of other inputs
     attn = torch.from_numpy(C.inputs(cfg.input_seed + 1, cfg.T).copy() * 0.01).cuda()
     stream = torch.cuda.current_stream().cuda_stream
+    stacked = cfg.n_layers > 1
+    turn = [0]
+
+    def fwd(L, st=stream):
+        if residual:
+            L.forward_residual(x.data_ptr(), attn.data_ptr(), cfg.T, cfg.K, stream=st)
+        else:
+            L.forward(x.data_ptr(), cfg.T, cfg.K, stream=st)
 
     def eager_step():
-        for L in layers:
-            if residual:
-                L.forward_residual(x.data_ptr(), attn.data_ptr(), cfg.T, cfg.K, stream=stream)
-            else:
-                L.forward(x.data_ptr(), cfg.T, cfg.K, stream=stream)
+        if stacked:
+            for L in layers:
+                fwd(L)
+        else:
+            fwd(layers[turn[0] % n_inst])
+            turn[0] += 1
 
     step = eager_step
     if use_graph:
-        # one graph per step: every layer's kernels, replayed as one launch
+        # one graph per step (a stacked config: every layer's kernels), replayed as one launch
+        assert stacked or n_inst == 1, "--graph times one layer or a stack"
         eager_step()
         torch.cuda.synchronize()
         graph, side = torch.cuda.CUDAGraph(), torch.cuda.Stream()
@@ -171,7 +203,7 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
                 for L in layers:
-                    L.forward(x.data_ptr(), cfg.T, cfg.K, stream=side.cuda_stream)
+                    fwd(L, side.cuda_stream)
         torch.cuda.current_stream().wait_stream(side)
         step = graph.replay
 
@@ -212,7 +244,7 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
     # launch duration of the dominant kernel: replayed back to back on the launch
     # stream between two HIP events, after the timed forwards
     reps = max(10, min(steps, 2000))
-    launch_us = layers[-1].time_stage(dom, reps, stream=stream)
+    launch_us = H.layers_time_stage(layers, dom, reps, stream=stream)
     achieved = dom_bytes / (launch_us * 1e-6) / 1e9
     # the kernel's binding roofline: its arithmetic intensity against the
     # machine balance (2.5 PFLOP/s dense fp16 MFMA over 8 TB/s = 312 flop/B)
@@ -239,8 +271,22 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
         | dict(traffic=measured_traffic(f"config{cfg.index}:{cfg.name}", kernel),
                bytes_per_launch=int(dom_bytes), flops_per_launch=int(dom_flops),
                launch_us=round(launch_us, 3),
-               launch_timing=f"HIP events around {reps} back-to-back launches"),
+               launch_timing=f"HIP events around {reps} back-to-back launches over "
+                             f"{len(layers)} resident layer(s) in rotation"),
     )
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(torch, H, C, cfg, seconds, shared_q8=False):
@@ -275,6 +321,9 @@ def cpu_baseline(torch, H, C, cfg, seconds, shared_q8=False):
         if el >= seconds or n >= 100000:
             break
     return dict(value=round(n / el, 3), unit="tokens/s", cores=cores, kind=kind,
+                cpu_model=cpu_model(),
+                prefill_note="hy3.c runs a prefill's MoE one token at a time (hy3_gpu.cu:836-837, "
+                             "hy3.c per-token forward), so its prefill tokens/s equals this rate",
                 sample=f"{n} tokens of config {cfg.index}, one at a time as hy3.c runs its MoE "
                        f"(forward_layer_moe per token), {el:.1f} s")
 
@@ -306,10 +355,11 @@ def main():
     if a.tokens:
         cfg = dataclasses.replace(cfg, T=a.tokens, name=f"{cfg.name}@T{a.tokens}")
     steps = a.steps or default_steps(cfg.T, cfg.n_layers)
+    rotate = a.rotate if cfg.n_layers == 1 else 1
     r = measure(torch, H, C, cfg, steps, a.warmup, use_graph=a.graph, path=a.path,
-                shared_q8=a.shared_q8, residual=a.residual)
+                shared_q8=a.shared_q8, residual=a.residual, rotate=rotate)
     out = {
-        "metric": "MoE-layer tokens/s (decode B=1) and achieved HBM GB/s vs peak",
+        "metric": "MoE-layer tokens/s at decode B=1 and 512-tok prefill; achieved HBM GB/s vs peak",
         "value": round(r["tokens_per_s"], 2),
         "unit": "tokens/s",
         "n_gpus": 1, "steps": steps, "warmup": a.warmup,
@@ -320,6 +370,11 @@ def main():
         "config": {"workload": f"config{cfg.index}:{cfg.name}", "tokens": cfg.T,
                    "layers": cfg.n_layers, "top_k": cfg.K, "experts": "192+1 shared",
                    "hidden": 4096, "ffn": 1536, "parallelism": "single-gpu",
+                   "timing": (f"cold: {rotate} resident layers "
+                              f"({rotate * 2.05:.1f} GB of Q4_K) in rotation, one per step"
+                              if rotate > 1 else
+                              "stack: every layer per step" if cfg.n_layers > 1 else
+                              "one layer re-run every step"),
                    "launch": "hip-graph" if a.graph else "direct",
                    "expert_path": ["auto", "gemv", "mfma", "mfma-narrow", "mfma-wide"][a.path],
                    "shared_expert": "q8_0" if a.shared_q8 else "q4_k",
@@ -329,6 +384,23 @@ def main():
                   "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},
         "roofline": r["roofline"],
     }
+    if cfg.index == 0 and not a.no_prefill and not a.tokens:
+        # the metric's second half: one 512-token prefill chunk (config 2)
+        c2 = C.CONFIGS[2]
+        steps2 = default_steps(c2.T, 1)
+        rp = measure(torch, H, C, c2, steps2, 5, path=a.path, shared_q8=a.shared_q8)
+        out["prefill"] = {
+            "workload": f"config{c2.index}:{c2.name}", "tokens": c2.T, "steps": steps2,
+            "tokens_per_s": round(rp["tokens_per_s"], 1),
+            "ms_per_step": round(rp["ms_per_step"], 4),
+            "experts_touched": round(rp["U"], 1),
+            "GB_per_s": round(rp["layer_GBps"], 1),
+            "hbm_frac": round(rp["layer_GBps"] / PEAK_HBM_GBS, 4),
+            "TFLOP_per_s": round(rp["layer_TFLOPs"], 2),
+            "mfma_frac": round(rp["layer_TFLOPs"] / PEAK_MFMA_TFLOPS, 4),
+            "stage_us": {k: round(v, 1) for k, v in rp["stage_us"].items()},
+            "roofline": rp["roofline"]}
+        torch.cuda.empty_cache()
     if a.secondary:
         sec = {}
         for c in C.CONFIGS:

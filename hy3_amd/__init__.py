@@ -66,6 +66,8 @@ _SIGS = {
     "hy3x_layer_set_rms_scale": (I32, [P, P, I32]),
     "hy3x_layer_last_path": (I32, [P, ctypes.POINTER(ctypes.c_int)]),
     "hy3x_layer_time_stage": (I32, [P, I32, I32, P, ctypes.POINTER(ctypes.c_float)]),
+    "hy3x_layers_time_stage": (I32, [ctypes.POINTER(P), I32, I32, I32, P,
+                                     ctypes.POINTER(ctypes.c_float)]),
     "hy3x_diag_read_rate": (I32, [P, I64, I64, I32, P, ctypes.POINTER(ctypes.c_float)]),
     "hy3x_layer_set_timing": (I32, [P, I32]),
     "hy3x_layer_set_trace": (I32, [P, I32, P]),
@@ -145,6 +147,16 @@ def gguf_check_layer(path, layer_index):
     return t.value
 
 
+def layers_time_stage(layers, stage, reps, stream=None):
+    """Mean µs per launch of one stage's kernels replayed over `layers` in rotation
+    (hy3x_layers_time_stage)."""
+    arr = (P * len(layers))(*[L._h for L in layers])
+    us = ctypes.c_float()
+    _check(lib().hy3x_layers_time_stage(arr, len(layers), MoELayer.STAGES.index(stage), reps,
+                                        stream, ctypes.byref(us)))
+    return us.value
+
+
 def read_rate_us(pool_ptr, pool_bytes, nbytes, reps=200, stream=None):
     """Mean µs per launch of a plain streaming read of nbytes (hy3x_diag_read_rate)."""
     us = ctypes.c_float()
@@ -155,9 +167,15 @@ def read_rate_us(pool_ptr, pool_bytes, nbytes, reps=200, stream=None):
 class MoELayer:
     """One Hy3 MoE FFN layer resident on the current HIP device."""
 
-    def __init__(self, max_tokens):
+    def __init__(self, max_tokens, share_scratch_with=None):
+        """share_scratch_with: another MoELayer whose forward scratch this layer
+        shares (hy3x_layer_create_shared; forwards of the two must not overlap)."""
         h = P()
-        _check(lib().hy3x_layer_create(ctypes.byref(h), max_tokens))
+        if share_scratch_with is not None:
+            _check(lib().hy3x_layer_create_shared(ctypes.byref(h), share_scratch_with._h))
+            max_tokens = share_scratch_with.max_tokens
+        else:
+            _check(lib().hy3x_layer_create(ctypes.byref(h), max_tokens))
         self._h = h
         self.max_tokens = max_tokens
 

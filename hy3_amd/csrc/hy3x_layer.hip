@@ -654,16 +654,20 @@ static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float 
   return HY3X_OK;
 }
 
-int hy3x_layer_time_stage(hy3x_layer *L, int stage, int reps, void *stream, float *us) {
-  if (!L || !us || reps < 1) return fail(HY3X_E_ARG, "bad argument");
+int hy3x_layers_time_stage(hy3x_layer *const *layers, int n, int stage, int reps, void *stream,
+                           float *us) {
+  if (!layers || n < 1 || !us || reps < 1) return fail(HY3X_E_ARG, "bad argument");
   if (stage < HY3X_STAGE_ROUTER || stage > HY3X_STAGE_COMBINE)
     return fail(HY3X_E_ARG, "stage %d outside [0,4]", stage);
-  if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
+  for (int i = 0; i < n; i++) {
+    if (!layers[i]) return fail(HY3X_E_ARG, "layer %d is NULL", i);
+    if (!layers[i]->last_T) return fail(HY3X_E_STATE, "layer %d: no forward yet", i);
+  }
   hipStream_t st = (hipStream_t)stream;
   EventPair ev;
   HIP_TRY(ev.create());
   HIP_TRY(hipEventRecord(ev.a, st));
-  for (int i = 0; i < reps; i++) launch_stage(L, stage, st);
+  for (int i = 0; i < reps; i++) launch_stage(layers[i % n], stage, st);
   HIP_TRY(hipEventRecord(ev.b, st));
   HIP_TRY(hipEventSynchronize(ev.b));
   float ms = 0.0f;
@@ -671,6 +675,10 @@ int hy3x_layer_time_stage(hy3x_layer *L, int stage, int reps, void *stream, floa
   HIP_TRY(hipGetLastError());
   *us = ms * 1e3f / reps;
   return HY3X_OK;
+}
+
+int hy3x_layer_time_stage(hy3x_layer *L, int stage, int reps, void *stream, float *us) {
+  return hy3x_layers_time_stage(&L, 1, stage, reps, stream, us);
 }
 
 int hy3x_layer_set_timing(hy3x_layer *L, int enable) {

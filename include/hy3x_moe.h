@@ -200,6 +200,11 @@ int hy3x_layer_stage_times(hy3x_layer *layer, float *ms, int n_stages, int *n_fo
  * the down stage of a single-token forward adds its output into x again, so x
  * is modified. No reference counterpart (measurement only). */
 int hy3x_layer_time_stage(hy3x_layer *layer, int stage, int reps, void *stream, float *us);
+/* The same over n layers in rotation (launch i replays layers[i % n]'s stage),
+ * so that with n layers whose weights together exceed the last-level cache
+ * every launch streams its weights from HBM. */
+int hy3x_layers_time_stage(hy3x_layer *const *layers, int n, int stage, int reps, void *stream,
+                           float *us);
 
 /* Diagnostics: the reference point for the roofline fractions. Mean
  * microseconds per launch of a plain streaming-read kernel reading `bytes`
