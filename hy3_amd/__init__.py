@@ -33,7 +33,8 @@ ROUTE_SCALE = 2.826
 T_X, T_NORM, T_ROUTER, T_BIAS, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-lib_path = os.path.join(_HERE, "libhy3x.so")
+# HY3X_LIBRARY names another build of the same library (A/B measurements)
+lib_path = os.environ.get("HY3X_LIBRARY") or os.path.join(_HERE, "libhy3x.so")
 _lib = None
 
 P = ctypes.c_void_p
