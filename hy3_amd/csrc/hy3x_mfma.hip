@@ -214,10 +214,14 @@ __device__ __forceinline__ void issue_b(const TileState<GATEUP, NTT> &st, int kb
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int buf = kb & 1;
   const uint8_t *bb = st.bbase + (size_t)kb * QK * 2;
+  // only the token rows the tile's NTT token tiles read: a copy covers two
+  // rows (copy j of wave w: rows 2 (B_DMA w + j), +1), a wave's sums lanes
+  // S_LANES / 4 rows (the skip is wave-uniform)
 #pragma unroll
   for (int j = 0; j < B_DMA; j++)
-    dma16_s(bb, st.boff[j], lds_addr(&bt_st[buf][0][0] + 64 * (B_DMA * wave + j)));
-  if (lane < S_LANES)
+    if (2 * (B_DMA * wave + j) < 16 * NTT)
+      dma16_s(bb, st.boff[j], lds_addr(&bt_st[buf][0][0] + 64 * (B_DMA * wave + j)));
+  if (lane < S_LANES && S_LANES * wave / 4 < 16 * NTT)
     dma16_s(st.sbase + (size_t)kb * 64, st.soff,
             lds_addr(&bm_st[buf][0][0] + S_LANES * wave));
 }
@@ -471,7 +475,9 @@ __device__ __forceinline__ void issue_b_q8(const TileStateQ8<GATEUP, NTT> &st, i
   const u4_t *dst = &bt_st[kb & 1][0][0];
   const uint8_t *bb = st.bbase + (size_t)kb * Q8K * 2;
 #pragma unroll
-  for (int j = 0; j < B8_DMA; j++) dma16_s(bb, st.boff[j], lds_addr(dst + 64 * (B8_DMA * wave + j)));
+  for (int j = 0; j < B8_DMA; j++)  // a copy covers four rows; only the rows the NTT tiles read
+    if (4 * (B8_DMA * wave + j) < 16 * NTT)
+      dma16_s(bb, st.boff[j], lds_addr(dst + 64 * (B8_DMA * wave + j)));
 }
 
 // fp16 weights (exact q) of 8 consecutive bytes, in the staged activations'
