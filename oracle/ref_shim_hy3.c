@@ -12,7 +12,11 @@
  *    ggml type, for which mul_mat_f32 writes zeros, hy3.c:1149-1152). The MoE
  *    half (hy3.c:1266-1325) is the reference's code, unmodified. After each
  *    token the router scores sigmoid+bias (scratch2[0..191], written at
- *    hy3.c:1272-1277 and not overwritten later) are copied out.
+ *    hy3.c:1272-1277 and not overwritten later) are copied out;
+ *  - hy3ref_model_load / hy3ref_model_moe / hy3ref_model_free: the engine's
+ *    own GGUF loader (hy3.c:805) and forward_layer_moe on the model it loads,
+ *    so the GPU drop-in can be initialised from the very hy3_model the
+ *    engine would hand it.
  */
 #include "hy3.c"
 
@@ -125,3 +129,44 @@ int hy3ref_moe_forward(float *x, int T, int K, const float *norm_w, const float 
   return hy3ref_moe_forward_t(x, T, K, norm_w, router, bias, has_bias, gate, up, down,
                               scores_out, quiet, 12);
 }
+
+/* ---- the reference's own loader (hy3.c:805-914) --------------------------
+ * hy3ref_model_load maps a GGUF file with hy3_model_load, exactly as the
+ * engine does, and adds the KV cache that the engine's context set-up would
+ * (hy3_model_load leaves cache_k / cache_v NULL; forward_layer_moe writes one
+ * position per call). k > 0 overrides n_expert_used like HY3_TOP_K_EXPERTS
+ * (hy3.c:824-833). The whole-file prefault (hy3.c:856-867) is skipped: it is
+ * a residency measure for zero-copy GPU mappings, not part of the numerics.
+ * Returns the hy3_model (opaque to the caller) or NULL. */
+void *hy3ref_model_load(const char *path, int n_threads, int k) {
+  setenv("HY3_NO_PREFAULT", "1", 1);
+  hy3_model *m = NULL;
+  if (hy3_model_load(&m, path, n_threads) != 0 || !m) return NULL;
+  if (k >= 1 && k <= HY3_N_EXPERT_USED) m->n_expert_used = k;
+  m->cache_k = (float *)calloc((size_t)4 * HY3_N_KV_HEAD * HY3_HEAD_DIM, sizeof(float));
+  m->cache_v = (float *)calloc((size_t)4 * HY3_N_KV_HEAD * HY3_HEAD_DIM, sizeof(float));
+  return m;
+}
+
+/* Runs forward_layer_moe(m, il, 0) (hy3.c:1219) on each of T rows of x in
+ * place, with an empty KV cache per row, so a file whose attention weights
+ * are zero contributes exactly +0 from the attention half. scores_out: [T x
+ * 192] sigmoid+bias router scores or NULL. Returns 0, -1 on a bad layer. */
+int hy3ref_model_moe(void *mp, int il, float *x, int T, float *scores_out) {
+  hy3_model *m = (hy3_model *)mp;
+  if (!m || il < HY3_N_LAYER_DENSE || il >= HY3_N_LAYER) return -1;
+  float *saved = m->embed;
+  for (int t = 0; t < T; t++) {
+    m->embed = x + (size_t)t * HY3_N_EMBD;
+    m->cache_len = 0;
+    forward_layer_moe(m, il, 0);
+    if (scores_out) memcpy(scores_out + (size_t)t * HY3_N_EXPERT, m->scratch2, HY3_N_EXPERT * sizeof(float));
+  }
+  m->embed = saved;
+  return 0;
+}
+
+int hy3ref_model_n_expert_used(void *mp) { return ((hy3_model *)mp)->n_expert_used; }
+
+/* hy3_model_free (hy3.c:924-949); the GPU context must be released first. */
+void hy3ref_model_free(void *mp) { hy3_model_free((hy3_model *)mp); }

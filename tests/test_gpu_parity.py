@@ -611,17 +611,32 @@ def test_forward_residual_rejects_alias(torch, layer):
         layer.forward_residual(xd.data_ptr(), xd.data_ptr(), 1)
 
 
-def test_load_gguf_layer_matches_source(torch, q8_layer, cpu, q8_mats, tmp_path):
-    """A whole layer written as a hy3 GGUF file (the converter's framing, tensor
-    names and types: Q4_K routed experts, Q8_0 shared expert, F32 router, norm
-    and bias) and loaded by hy3x_layer_load_gguf computes exactly what the
-    layer it came from computes (T = 1 and T = 40)."""
+GGUF_IL = 1  # the first MoE layer (hy3.h: HY3_N_LAYER_DENSE = 1)
+
+
+@pytest.fixture(scope="module")
+def layer_gguf(cpu, q8_mats, tmp_path_factory):
+    """The test layer written as a hy3 GGUF file with the converter's framing,
+    tensor names and types (Q4_K routed experts, Q8_0 shared expert, F32
+    router, norm and bias) at layer GGUF_IL, plus what the engine's loader
+    requires of a whole model (hy3.c:889-898: token_embd.weight of [120832,
+    4096], output.weight) and layer GGUF_IL's attention weights, all zero and
+    written sparsely: zero Q8_0 blocks make the attention half add exactly
+    +0 in hy3.c's forward_layer_moe (hy3.c:1226-1262)."""
     import sys
     sys.path.insert(0, G)
     from gguf_write import write_gguf
     nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
-    il = 7
-    t = [(f"blk.{il}.ffn_norm.weight", 0, [D], nw.view(np.uint8)),
+    il = GGUF_IL
+    t = [("token_embd.weight", 1, [120832, D], None),
+         ("output_norm.weight", 0, [D], None),
+         ("output.weight", 8, [120832, D], None),
+         (f"blk.{il}.attn_norm.weight", 0, [D], None),
+         (f"blk.{il}.attn_q.weight", 8, [64 * 128, D], None),
+         (f"blk.{il}.attn_k.weight", 8, [8 * 128, D], None),
+         (f"blk.{il}.attn_v.weight", 8, [8 * 128, D], None),
+         (f"blk.{il}.attn_output.weight", 8, [D, 64 * 128], None),
+         (f"blk.{il}.ffn_norm.weight", 0, [D], nw.view(np.uint8)),
          (f"blk.{il}.ffn_gate_inp.weight", 0, [E, D], rt.view(np.uint8)),
          (f"blk.{il}.ffn_gate_exps_b.bias", 0, [E], b.view(np.uint8))]
     kinds = ("gate", "up", "down")
@@ -633,12 +648,19 @@ def test_load_gguf_layer_matches_source(torch, q8_layer, cpu, q8_mats, tmp_path)
     for m, kind in enumerate(kinds):
         dims = [D, 1536] if kind == "down" else [1536, D]
         t.append((f"blk.{il}.ffn_{kind}_shexp.weight", 8, dims, q8_mats[m]))
-    path = tmp_path / "layer.gguf"
+    path = tmp_path_factory.mktemp("gguf") / "hy3_layer.gguf"
     write_gguf(path, t)
-    assert H.gguf_check_layer(path, il) == 8
+    yield path
+    path.unlink()
+
+
+def test_load_gguf_layer_matches_source(torch, q8_layer, layer_gguf):
+    """A whole layer loaded from a hy3 GGUF file by hy3x_layer_load_gguf
+    computes exactly what the layer it came from computes (T = 1 and T = 40)."""
+    assert H.gguf_check_layer(layer_gguf, GGUF_IL) == 8
     L2 = H.MoELayer(64)
     try:
-        L2.load_gguf(path, il)
+        L2.load_gguf(layer_gguf, GGUF_IL)
         for T in (1, 40):
             x = O.normal(T * D, O.key(0xC2, 0, O.T_X), 1.0).reshape(T, D)
             y1 = run(torch, q8_layer, x)[0]
@@ -646,4 +668,57 @@ def test_load_gguf_layer_matches_source(torch, q8_layer, cpu, q8_mats, tmp_path)
             assert np.array_equal(y1, y2), T
     finally:
         L2.close()
-        path.unlink()
+
+
+REF_LIB = os.path.join(os.path.dirname(G), "..", "oracle", "_ref", "libhy3ref.so")
+ENGINE_LIB = os.path.join(os.path.dirname(G), "..", "hy3_amd", "engine", "_build",
+                          "libhy3gpu_moe.so")
+
+
+@pytest.mark.skipif(not (os.path.exists(REF_LIB) and os.path.exists(ENGINE_LIB)),
+                    reason="needs oracle/_ref and the engine drop-in (built where the "
+                           "reference sources are present)")
+@pytest.mark.parametrize("K", [8, 4])
+def test_engine_loader_drop_in_matches_reference(torch, q8_layer, layer_gguf, K):
+    """End to end through the engine's own objects: the file is loaded by
+    hy3.c's hy3_model_load (hy3.c:805), the GPU drop-in is initialised from
+    that hy3_model by hy3_gpu_init and run by hy3_gpu_ffn_moe_host, and
+    hy3.c's forward_layer_moe runs on the same hy3_model on the host. The
+    drop-in equals the library layer bit for bit (it bound the very tensors
+    the loader mapped, with n_expert_used = K as HY3_TOP_K_EXPERTS sets it),
+    and is within TOL of the reference, with the reference's top-K experts
+    (from its recorded router scores, hy3.c:1272-1282) equal to the layer's."""
+    import ctypes
+    ref = ctypes.CDLL(REF_LIB)
+    ref.hy3ref_model_load.restype = ctypes.c_void_p
+    ref.hy3ref_model_load.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int]
+    ref.hy3ref_model_moe.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_void_p]
+    ref.hy3ref_model_n_expert_used.argtypes = [ctypes.c_void_p]
+    ref.hy3ref_model_free.argtypes = [ctypes.c_void_p]
+    eng = ctypes.CDLL(ENGINE_LIB)
+    eng.hy3_gpu_init.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    eng.hy3_gpu_free.argtypes = [ctypes.c_void_p]
+    eng.hy3_gpu_ffn_moe_host.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_int]
+    m = ref.hy3ref_model_load(str(layer_gguf).encode(), 16, K)
+    assert m
+    try:
+        assert ref.hy3ref_model_n_expert_used(m) == K
+        assert eng.hy3_gpu_init(m, GGUF_IL + 1) == 0
+        for T, seed in ((1, 0xE1), (5, 0xE2), (24, 0xE3)):
+            x = O.normal(T * D, O.key(seed, 0, O.T_X), 1.0).reshape(T, D)
+            y_gpu = np.ascontiguousarray(x.copy())
+            assert eng.hy3_gpu_ffn_moe_host(m, GGUF_IL, y_gpu.ctypes.data, T) == 0
+            y_lib, ids, _, _ = run(torch, q8_layer, x, K)
+            assert np.array_equal(y_gpu.view(np.uint32), y_lib.view(np.uint32)), T
+            y_ref = np.ascontiguousarray(x.copy())
+            scores = np.zeros((T, E), np.float32)
+            assert ref.hy3ref_model_moe(m, GGUF_IL, y_ref.ctypes.data, T,
+                                        scores.ctypes.data) == 0
+            ids_ref = np.argsort(-scores, axis=1, kind="stable")[:, :K]
+            assert np.array_equal(np.sort(ids, 1), np.sort(ids_ref, 1)), T
+            assert O.rel_l2(y_gpu - x, y_ref - x) <= TOL, T
+    finally:
+        eng.hy3_gpu_free(m)
+        ref.hy3ref_model_free(m)
