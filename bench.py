@@ -59,9 +59,10 @@ def parse():
     p.add_argument("--no-prefill", action="store_true",
                    help="skip the 512-token prefill entry (config 2) of the default line")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--path", type=int, default=0, choices=(0, 1, 2, 3, 4),
+    p.add_argument("--path", type=int, default=0, choices=(0, 1, 2, 3, 4, 5),
                    help="expert path: 0 the library's choice by T, 1 GEMV tiles, 2 MFMA tiles, "
-                        "3 / 4 MFMA with the narrow (32-token) / wide (64-token) tile shape")
+                        "3 / 4 MFMA with the narrow (32-token) / wide (64-token) tile shape, "
+                        "5 MFMA with 128-token tiles")
     p.add_argument("--tokens", type=int, default=0,
                    help="override the config's token count (tuning sweeps)")
     p.add_argument("--shared-q8", action="store_true",
@@ -144,6 +145,8 @@ def dominant_kernel(stage, last_path):
     (hy3x_layer_last_path)."""
     if last_path == 0:
         return {"gateup": "k_gateup_decode", "down": "k_down_decode"}[stage]
+    if last_path == 5:
+        return {"gateup": "mfma_big::k_moe_big<true>", "down": "mfma_big::k_moe_big<false>"}[stage]
     if last_path in (3, 4):
         ns = "mfma_wide" if last_path == 4 else "mfma_narrow"
         return {"gateup": f"{ns}::k_moe_mfma<true>", "down": f"{ns}::k_moe_mfma<false>"}[stage]
@@ -376,7 +379,7 @@ def main():
                               "stack: every layer per step" if cfg.n_layers > 1 else
                               "one layer re-run every step"),
                    "launch": "hip-graph" if a.graph else "direct",
-                   "expert_path": ["auto", "gemv", "mfma", "mfma-narrow", "mfma-wide"][a.path],
+                   "expert_path": ["auto", "gemv", "mfma", "mfma-narrow", "mfma-wide", "mfma-big"][a.path],
                    "shared_expert": "q8_0" if a.shared_q8 else "q4_k",
                    "entry": "forward_residual" if a.residual else "forward"},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),

@@ -75,6 +75,7 @@ struct hy3x_layer {
     float scale = 1.0f;
     Mode mode = Mode::GEMV;
     bool wide = false;  // MFMA mode: the wide tile shape (mfma_wide)
+    bool big = false;   // MFMA mode: 128-token tiles (mfma_big)
     const float *r_in = nullptr;  // substituted RMSNorm scales, or null
     Scratch sc;         // the scratch this forward runs on
   } cur;
@@ -173,6 +174,11 @@ constexpr int kMfmaMinT = 2;
 // 4096 (Zipf routing): 3.36 vs 2.62 -- with few tokens per expert the tiles are
 // mostly empty and one workgroup per CU hides less latency than two.
 constexpr int kMfmaWideMinT = 384;
+// From this many tokens (Q4_K shared expert) the MFMA GEMMs use 128-token tiles
+// (mfma_big). Measured on MI355X (ms per layer, wide vs 128-token tiles):
+// 1024 tokens 0.93 vs 0.97, 2048: 1.49 vs 1.41, 3072: 2.05 vs 1.97, 4096: 2.60
+// vs 2.46, 4096 with Zipf routing: 2.58 vs 2.34-2.38.
+constexpr int kMfmaBigMinT = 2048;
 
 static constexpr int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
@@ -455,7 +461,7 @@ int hy3x_layer_set_rms_scale(hy3x_layer *L, const float *r, int n) {
 }
 
 int hy3x_layer_set_path(hy3x_layer *L, int path) {
-  if (!L || path < 0 || path > 4) return fail(HY3X_E_ARG, "bad path");
+  if (!L || path < 0 || path > 5) return fail(HY3X_E_ARG, "bad path");
   L->path = path;
   return HY3X_OK;
 }
@@ -464,7 +470,7 @@ int hy3x_layer_last_path(const hy3x_layer *L, int *path) {
   if (!L || !path) return fail(HY3X_E_ARG, "NULL argument");
   if (!L->last_T) return fail(HY3X_E_STATE, "no forward yet");
   const auto &c = L->cur;
-  *path = c.mode == Mode::DECODE ? 0 : c.mode == Mode::GEMV ? 1 : c.wide ? 4 : 3;
+  *path = c.mode == Mode::DECODE ? 0 : c.mode == Mode::GEMV ? 1 : c.big ? 5 : c.wide ? 4 : 3;
   return HY3X_OK;
 }
 
@@ -531,6 +537,9 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         k_gateup_decode<<<K * DEC_GU_BLOCKS, 64 * DEC_GU_WAVES, 0, st>>>(L->wq, S.s16, S.sig, S.score, K,
                                                           c.scale, S.ids, S.wpre, S.w,
                                                           L->stats, S.h16, L->trace[1]);
+      else if (c.mode == Mode::MFMA && c.big)
+        mfma_big::k_moe_big<true><<<mt * (F / (16 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
+            L->wq, S.s16m, S.ssum, S.list, S.tiles, S.n_tiles, T, K, S.h16m, nullptr);
       else if (c.mode == Mode::MFMA && c.wide)
         mfma_wide::k_moe_mfma<true>
             <<<mt * (F / mfma_wide::ROWS_GU), 64 * mfma_wide::WAVES, 0, st>>>(
@@ -553,7 +562,10 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(S.h16m, S.hsum);
         const uint8_t *wsh = L->shared_q8 ? L->wsh : nullptr;
-        if (c.wide)
+        if (c.big)
+          mfma_big::k_moe_big<false><<<mt * (D / (32 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
+              L->wq, S.h16m, S.hsum, S.list, S.tiles, S.n_tiles, T, K, nullptr, S.out);
+        else if (c.wide)
           mfma_wide::k_moe_mfma<false>
               <<<mt * (D / (2 * mfma_wide::ROWS_GU)), 64 * mfma_wide::WAVES, 0, st>>>(
                   L->wq, wsh, S.h16m, S.hsum, S.list, S.tiles, S.n_tiles, T, K, nullptr,
@@ -634,10 +646,17 @@ static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float 
     c.mode = Mode::GEMV;
   if (L->shared_q8 && c.mode == Mode::GEMV)
     return fail(HY3X_E_STATE, "the GEMV tile path needs a Q4_K shared expert");
-  c.wide = c.mode == Mode::MFMA &&
+  c.big = c.mode == Mode::MFMA &&
+          (L->path == 5 || ((L->path == 0 || L->path == 2) && T >= kMfmaBigMinT && !L->shared_q8));
+  if (c.big && L->shared_q8)
+    return fail(HY3X_E_STATE, "the 128-token tiles need a Q4_K shared expert");
+  c.wide = c.mode == Mode::MFMA && !c.big &&
            (L->path == 4 || (L->path != 3 && T >= kMfmaWideMinT));
   // tokens per work tile
-  c.nt = c.mode != Mode::MFMA ? 4 : c.wide ? mfma_wide::TOKENS : mfma_narrow::TOKENS;
+  c.nt = c.mode != Mode::MFMA ? 4
+         : c.big              ? BIG_TOKENS
+         : c.wide             ? mfma_wide::TOKENS
+                              : mfma_narrow::TOKENS;
   c.mt = std::min(max_tiles_for(T, K, c.nt), sc->max_tiles);
   record_stage(L, st, -1);
   for (int stage = HY3X_STAGE_ROUTER; stage <= HY3X_STAGE_COMBINE; stage++) {

@@ -391,17 +391,17 @@ def test_routing_with_ties(torch, T, case):
 @pytest.mark.parametrize("T", [1, 7, 64, 200, 400])
 def test_expert_paths_match_oracle(torch, layer, cpu, T):
     """Every expert path (0 automatic, 1 wavefront GEMV, 2 MFMA grouped GEMM,
-    3 / 4 its narrow / wide tile shape) meets the tolerance on the same
+    3 / 4 its narrow / wide tile shape, 5 its 128-token tiles) meets the tolerance on the same
     tokens; routing is identical on all; hy3x_layer_last_path reports the
     path that ran (automatic: decode kernels at T = 1, the narrow MFMA shape
-    below 384 tokens, the wide one from there)."""
+    below 384 tokens, the wide one from there, 128-token tiles from 2048)."""
     x = C.inputs(0xC2, T, first_token=300)
     rows = np.linspace(0, T - 1, min(T, 6)).astype(int)
     yo, ro = cpu.forward(x[rows])
-    mfma_auto = 4 if T >= 384 else 3
-    ran = {0: 0 if T == 1 else mfma_auto, 1: 1, 2: mfma_auto, 3: 3, 4: 4}
+    mfma_auto = 5 if T >= 2048 else 4 if T >= 384 else 3
+    ran = {0: 0 if T == 1 else mfma_auto, 1: 1, 2: mfma_auto, 3: 3, 4: 4, 5: 5}
     try:
-        for path in (0, 1, 2, 3, 4):
+        for path in (0, 1, 2, 3, 4, 5):
             layer.set_path(path)
             y, ids, _, _ = run(torch, layer, x)
             assert layer.last_path() == ran[path], path
@@ -411,13 +411,32 @@ def test_expert_paths_match_oracle(torch, layer, cpu, T):
         layer.set_path(0)
 
 
+@pytest.mark.parametrize("T", [2, 40, 333, 1000, 4096])
+def test_big_tiles_equal_narrow_tiles(torch, layer, cpu, T):
+    """The 128-token tiles (activations staged per half block column, the
+    dequantised weights reused over up to eight 16-token groups) do per
+    element exactly the narrow tiles' arithmetic: the same output bit for bit,
+    on tiles of every size class (2, 4, 6 and 8 token groups)."""
+    x = C.inputs(0xC7, T)
+    try:
+        layer.set_path(3)
+        y3, ids3, _, _ = run(torch, layer, x)
+        layer.set_path(5)
+        y5, ids5, _, _ = run(torch, layer, x)
+        assert layer.last_path() == 5
+    finally:
+        layer.set_path(0)
+    assert np.array_equal(ids3, ids5)
+    assert np.array_equal(y3.view(np.uint32), y5.view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [40, 200])
 def test_mfma_tile_shapes_on_crowded_experts(torch, layer, cpu, T):
     """A bias of +50 on eight experts sends every token to them, so each of
-    those experts holds all T tokens: the narrow shape (32-token tiles) and the
+    those experts holds all T tokens: the narrow shape (32-token tiles), the
     wide one (64-token tiles: T = 40 is one tile of 40 tokens, three 16-token
     column groups; T = 200 is three full tiles of four groups and one of 8
-    tokens) give the same output bit for bit (the same per-element arithmetic
+    tokens) and the 128-token tiles give the same output bit for bit (the same per-element arithmetic
     in every 16-token group and either shape), within the tolerance of the
     oracle's."""
     nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
@@ -430,11 +449,12 @@ def test_mfma_tile_shapes_on_crowded_experts(torch, layer, cpu, T):
     x = C.inputs(0xC5, T)
     try:
         out = {}
-        for path in (3, 4):
+        for path in (3, 4, 5):
             layer.set_path(path)
             out[path], ids, _, _ = run(torch, layer, x)
             assert np.array_equal(np.sort(ids, axis=1), np.tile(np.sort(hot), (T, 1)))
         assert np.array_equal(out[3].view(np.uint32), out[4].view(np.uint32))
+        assert np.array_equal(out[3].view(np.uint32), out[5].view(np.uint32))
         rows = np.linspace(0, T - 1, 5).astype(int)
         yo, _ = cpu.forward(x[rows])
         assert O.rel_l2(out[4][rows] - x[rows], yo - x[rows]) <= TOL
