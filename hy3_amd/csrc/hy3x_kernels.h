@@ -101,19 +101,22 @@ extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, 
 HY3X_DECLARE_MFMA(mfma_narrow, 32, 4, 1)
 HY3X_DECLARE_MFMA(mfma_wide, 64, 8, 1)
 #undef HY3X_DECLARE_MFMA
-// 128-token tiles for experts holding many tokens (hy3x_mfma_big.hip; Q4_K
-// shared expert only): the MFMA tiles' arithmetic, each wave's dequantised
+// 128-token tiles for experts holding many tokens (hy3x_mfma_big.hip): the
+// MFMA tiles' arithmetic, each wave's dequantised
 // weights reused over up to eight 16-token column groups.
 constexpr int BIG_TOKENS = 128, BIG_WAVES = 8;
 namespace mfma_big {
 template <bool GATEUP>
 __global__ __launch_bounds__(64 * BIG_WAVES) void k_moe_big(
-    const uint8_t *wq, const __half *act, const __half *act_sum, const int32_t *list,
-    const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m, float *out);
-extern template __global__ void k_moe_big<true>(const uint8_t *, const __half *, const __half *,
+    const uint8_t *wq, const uint8_t *wsh, const __half *act, const __half *act_sum,
+    const int32_t *list, const int4 *tiles, const int32_t *n_tiles, int T, int K, __half *h16m,
+    float *out);
+extern template __global__ void k_moe_big<true>(const uint8_t *, const uint8_t *, const __half *,
+                                                const __half *,
                                                 const int32_t *, const int4 *, const int32_t *,
                                                 int, int, __half *, float *);
-extern template __global__ void k_moe_big<false>(const uint8_t *, const __half *, const __half *,
+extern template __global__ void k_moe_big<false>(const uint8_t *, const uint8_t *,
+                                                 const __half *, const __half *,
                                                  const int32_t *, const int4 *, const int32_t *,
                                                  int, int, __half *, float *);
 }  // namespace mfma_big

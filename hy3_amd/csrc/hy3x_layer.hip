@@ -174,7 +174,7 @@ constexpr int kMfmaMinT = 2;
 // 4096 (Zipf routing): 3.36 vs 2.62 -- with few tokens per expert the tiles are
 // mostly empty and one workgroup per CU hides less latency than two.
 constexpr int kMfmaWideMinT = 384;
-// From this many tokens (Q4_K shared expert) the MFMA GEMMs use 128-token tiles
+// From this many tokens the MFMA GEMMs use 128-token tiles
 // (mfma_big). Measured on MI355X (ms per layer, wide vs 128-token tiles):
 // 1024 tokens 0.93 vs 0.97, 2048: 1.49 vs 1.41, 3072: 2.05 vs 1.97, 4096: 2.60
 // vs 2.46, 4096 with Zipf routing: 2.58 vs 2.34-2.38.
@@ -539,7 +539,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                           L->stats, S.h16, L->trace[1]);
       else if (c.mode == Mode::MFMA && c.big)
         mfma_big::k_moe_big<true><<<mt * (F / (16 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
-            L->wq, S.s16m, S.ssum, S.list, S.tiles, S.n_tiles, T, K, S.h16m, nullptr);
+            L->wq, L->shared_q8 ? L->wsh : nullptr, S.s16m, S.ssum, S.list, S.tiles, S.n_tiles, T, K, S.h16m, nullptr);
       else if (c.mode == Mode::MFMA && c.wide)
         mfma_wide::k_moe_mfma<true>
             <<<mt * (F / mfma_wide::ROWS_GU), 64 * mfma_wide::WAVES, 0, st>>>(
@@ -564,7 +564,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         const uint8_t *wsh = L->shared_q8 ? L->wsh : nullptr;
         if (c.big)
           mfma_big::k_moe_big<false><<<mt * (D / (32 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
-              L->wq, S.h16m, S.hsum, S.list, S.tiles, S.n_tiles, T, K, nullptr, S.out);
+              L->wq, wsh, S.h16m, S.hsum, S.list, S.tiles, S.n_tiles, T, K, nullptr, S.out);
         else if (c.wide)
           mfma_wide::k_moe_mfma<false>
               <<<mt * (D / (2 * mfma_wide::ROWS_GU)), 64 * mfma_wide::WAVES, 0, st>>>(
@@ -647,9 +647,7 @@ static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float 
   if (L->shared_q8 && c.mode == Mode::GEMV)
     return fail(HY3X_E_STATE, "the GEMV tile path needs a Q4_K shared expert");
   c.big = c.mode == Mode::MFMA &&
-          (L->path == 5 || ((L->path == 0 || L->path == 2) && T >= kMfmaBigMinT && !L->shared_q8));
-  if (c.big && L->shared_q8)
-    return fail(HY3X_E_STATE, "the 128-token tiles need a Q4_K shared expert");
+          (L->path == 5 || ((L->path == 0 || L->path == 2) && T >= kMfmaBigMinT));
   c.wide = c.mode == Mode::MFMA && !c.big &&
            (L->path == 4 || (L->path != 3 && T >= kMfmaWideMinT));
   // tokens per work tile

@@ -402,19 +402,6 @@ __device__ __forceinline__ void issue_b_q8(const TileStateQ8<GATEUP, NTT> &st, i
       dma16_s(bb, st.boff[j], lds_addr(dst + 64 * (B8_DMA * wave + j)));
 }
 
-// fp16 weights (exact q) of 8 consecutive bytes, in the staged activations'
-// run order (0, 2, 1, 3, 4, 6, 5, 7).
-__device__ __forceinline__ h8_t q8_run(u2_t b) {
-  const uint32_t ex = 0x64646464u, a = b.x ^ 0x80808080u, c = b.y ^ 0x80808080u;
-  const h2_t m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-  u4_t w;
-  w.x = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, a, 0x04020400u)) + m1152);
-  w.y = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, a, 0x04030401u)) + m1152);
-  w.z = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, c, 0x04020400u)) + m1152);
-  w.w = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, c, 0x04030401u)) + m1152);
-  return __builtin_bit_cast(h8_t, w);
-}
-
 template <bool GATEUP, int NTT>
 __device__ __forceinline__ void mfma_step_q8(TileStateQ8<GATEUP, NTT> &st, int kb) {
   using S = TileStateQ8<GATEUP, NTT>;

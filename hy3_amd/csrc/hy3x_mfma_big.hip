@@ -21,6 +21,7 @@
 // Copies at step s (after its barrier): activations of step s + 1, then at
 // h = 0 the weights of column kb + 1, at h = 1 the sums of column kb + 1.
 #include "hy3x_mfma_ops.h"
+#include "hy3x_q8.h"
 
 namespace hy3x {
 namespace mfma_big {
@@ -67,6 +68,28 @@ struct State {
   f4_t dblk[C::RG][C::NMAT][NTT];  // the current column's block sums
   u4_t hdr[C::RG][C::NMAT];        // the current column's row-block headers
 };
+
+// Weight copy sources of the tile's row tile rt: wave w copies chunks
+// [288 w, 288 w + 288) of the column's (row-block c / 9, 16-byte piece c % 9),
+// 64 per copy. A column is one 144-byte block per row: Q4_K (256 of K) or the
+// shared expert's Q8 super-block (128 of K); mat_bytes is the matrix stride.
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void set_weights(State<GATEUP, NTT> &st, const uint8_t *base,
+                                            int64_t mat_bytes, int rt) {
+  using C = Cfg<GATEUP>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ncol = mat_bytes / ((int64_t)C::NROWS * QB);  // columns per row
+  st.abase = base;
+#pragma unroll
+  for (int j = 0; j < A_DMA; j++) {
+    int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
+    if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
+    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
+    const int m = GATEUP ? rb / (RB / 2) : 2, lrow = GATEUP ? rb % (RB / 2) : rb;
+    st.aoff[j] = (uint32_t)(m * mat_bytes + (int64_t)(rt * C::TROWS + lrow) * ncol * QB + 16 * pc);
+  }
+  st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
+}
 
 // Copies (wave-uniform counts): weights A_DMA, activations X_DMA (those
 // covering rows past the tile's 16 NTT are skipped), sums S_DMA (idem).
@@ -189,8 +212,70 @@ __device__ __forceinline__ void big_step(State<GATEUP, NTT> &st, int s) {
   }
 }
 
+
+// The shared expert in Q8 (q8x128 super-blocks, hy3x_q8.h): a column is one
+// 144-byte super-block per row (128 of K), i.e. one activation step of the
+// Q4_K tiles, so the copies are the same (issue_w / issue_x with step = Q8
+// column). Per column and row: four 32-weight blocks, each one 16x16x32 MFMA of
+// the exact integers q against the activations, scaled by its d in fp32:
+// acc += d_b * (x_b . q_b) -- the order of the MFMA tiles' mfma_step_q8.
+// Copies of column c + 1 are issued after the barrier of column c.
+template <bool GATEUP, int NTT>
+__device__ __forceinline__ void big_tile_q8_columns(State<GATEUP, NTT> &st) {
+  using C = Cfg<GATEUP>;
+  constexpr int RG = C::RG, NMAT = C::NMAT, NC = C::KD / Q8K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, g = lane >> 4;
+  const f4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  issue_w(st, 0);
+  issue_x(st, 0);
+  for (int c = 0; c < NC; c++) {
+    wait_copies_and_barrier<0>();
+    issue_w(st, c + 1 < NC ? c + 1 : NC - 1);  // past the end: a harmless re-copy
+    issue_x(st, c + 1 < NC ? c + 1 : NC - 1);
+    const u4_t *as = &a_ring[c & 1][0];
+    const u4_t *xs = &bx[c & 1][0];
+    f4_t dsc[RG][NMAT];
+    u2_t qb[RG][NMAT][4];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+      for (int m = 0; m < NMAT; m++) {
+        const int rb = (GATEUP ? m * (RB / 2) : 0) + 16 * (RG * wave + rg) + lr;
+        dsc[rg][m] = __builtin_bit_cast(f4_t, as[rb * RB_CHUNKS]);
+        const u2_t *qp = reinterpret_cast<const u2_t *>(as + rb * RB_CHUNKS + 1);
+#pragma unroll
+        for (int b = 0; b < 4; b++) qb[rg][m][b] = qp[4 * b + g];
+      }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      h8_t wf[RG][NMAT];
+#pragma unroll
+      for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) wf[rg][m] = q8_run(qb[rg][m][b]);
+#pragma unroll
+      for (int t = 0; t < NTT; t++) {
+        const h8_t x =
+            __builtin_bit_cast(h8_t, xs[16 * (16 * t + lr) + ((4 * b + g) ^ lr)]);
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++)
+#pragma unroll
+          for (int m = 0; m < NMAT; m++) {
+            const f4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, wf[rg][m], zero4, 0, 0, 0);
+            const float d = dsc[rg][m][b];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              st.acc[rg][m][t][i] = __builtin_fmaf(d, p[i], st.acc[rg][m][t][i]);
+          }
+      }
+    }
+  }
+}
+
 template <bool GATEUP, int NTT>
 __device__ __forceinline__ void big_tile(const uint8_t *__restrict__ wq,
+                                         const uint8_t *__restrict__ wsh,
                                          const __half *__restrict__ act,
                                          const __half *__restrict__ act_sum, int e, int n,
                                          int rt, __half *__restrict__ h16m,
@@ -200,18 +285,11 @@ __device__ __forceinline__ void big_tile(const uint8_t *__restrict__ wq,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, g = lane >> 4;
   State<GATEUP, NTT> st;
-  // weights: wave w copies chunks [288 w, 288 w + 288) of the column's
-  // (row-block c / 9, 16-byte piece c % 9), 64 per copy
-  st.abase = wq + (size_t)__builtin_amdgcn_readfirstlane(e) * EXPERT_BYTES;
-#pragma unroll
-  for (int j = 0; j < A_DMA; j++) {
-    int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
-    if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
-    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
-    const int m = GATEUP ? rb / (RB / 2) : 2, lrow = GATEUP ? rb % (RB / 2) : rb;
-    st.aoff[j] = (uint32_t)(m * MAT_BYTES + (rt * C::TROWS + lrow) * NKB * QB + 16 * pc);
-  }
-  st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
+  const bool q8 = wsh != nullptr && e == E;  // the shared expert in Q8 (uniform)
+  if (q8)
+    set_weights(st, wsh, Q8_MAT_BYTES, rt);
+  else
+    set_weights(st, wq + (size_t)__builtin_amdgcn_readfirstlane(e) * EXPERT_BYTES, MAT_BYTES, rt);
   // activations: copy j of wave w fills positions q = 64 (X_DMA w + j) + lane
   // of the 128 x 16 half-column tile: row r = q / 16, position q % 16 holds
   // chunk (q % 16) ^ (r & 15) of the half. Sums: positions q = 64 (S_DMA w +
@@ -240,14 +318,18 @@ __device__ __forceinline__ void big_tile(const uint8_t *__restrict__ wq,
 #pragma unroll
       for (int t = 0; t < NTT; t++) st.acc[rg][m][t] = zero4;
 
-  // prologue: the copies step 0 needs (weights and sums of column 0,
-  // activations of half 0)
-  issue_w(st, 0);
-  issue_s(st, 0);
-  issue_x(st, 0);
-  // two steps per iteration: the half h is a constant in each
+  if (q8) {
+    big_tile_q8_columns(st);
+  } else {
+    // prologue: the copies step 0 needs (weights and sums of column 0,
+    // activations of half 0)
+    issue_w(st, 0);
+    issue_s(st, 0);
+    issue_x(st, 0);
+    // two steps per iteration: the half h is a constant in each
 #pragma unroll 2
-  for (int s = 0; s < 2 * NKB; s++) big_step(st, s);
+    for (int s = 0; s < 2 * NKB; s++) big_step(st, s);
+  }
   // drain the trailing re-copies before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -272,10 +354,11 @@ __device__ __forceinline__ void big_tile(const uint8_t *__restrict__ wq,
 }
 
 // Grouped GEMM over a tile list of at most BIG_TOKENS tokens per tile,
-// operands and outputs as k_moe_mfma (Q4_K shared expert only).
+// operands and outputs as k_moe_mfma; wsh != nullptr: the shared expert's
+// tiles use its Q8 matrices.
 template <bool GATEUP>
 __global__ __launch_bounds__(B_THREADS) void k_moe_big(
-    const uint8_t *__restrict__ wq, const __half *__restrict__ act,
+    const uint8_t *__restrict__ wq, const uint8_t *__restrict__ wsh, const __half *__restrict__ act,
     const __half *__restrict__ act_sum, const int32_t *__restrict__ list,
     const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles, int T, int K,
     __half *__restrict__ h16m, float *__restrict__ out) {
@@ -294,19 +377,19 @@ __global__ __launch_bounds__(B_THREADS) void k_moe_big(
   }
   __syncthreads();
   if (n > 96)
-    big_tile<GATEUP, 8>(wq, act, act_sum, e, n, rt, h16m, out);
+    big_tile<GATEUP, 8>(wq, wsh, act, act_sum, e, n, rt, h16m, out);
   else if (n > 64)
-    big_tile<GATEUP, 6>(wq, act, act_sum, e, n, rt, h16m, out);
+    big_tile<GATEUP, 6>(wq, wsh, act, act_sum, e, n, rt, h16m, out);
   else if (n > 32)
-    big_tile<GATEUP, 4>(wq, act, act_sum, e, n, rt, h16m, out);
+    big_tile<GATEUP, 4>(wq, wsh, act, act_sum, e, n, rt, h16m, out);
   else
-    big_tile<GATEUP, 2>(wq, act, act_sum, e, n, rt, h16m, out);
+    big_tile<GATEUP, 2>(wq, wsh, act, act_sum, e, n, rt, h16m, out);
 }
 
-template __global__ void k_moe_big<true>(const uint8_t *, const __half *, const __half *,
+template __global__ void k_moe_big<true>(const uint8_t *, const uint8_t *, const __half *, const __half *,
                                          const int32_t *, const int4 *, const int32_t *, int,
                                          int, __half *, float *);
-template __global__ void k_moe_big<false>(const uint8_t *, const __half *, const __half *,
+template __global__ void k_moe_big<false>(const uint8_t *, const uint8_t *, const __half *, const __half *,
                                           const int32_t *, const int4 *, const int32_t *, int,
                                           int, __half *, float *);
 

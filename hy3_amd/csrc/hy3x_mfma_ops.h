@@ -94,4 +94,17 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return x * q + (x < r ? x : r) + i;
 }
 
+// fp16 weights (exact q) of 8 consecutive bytes, in the staged activations'
+// run order (0, 2, 1, 3, 4, 6, 5, 7).
+__device__ __forceinline__ h8_t q8_run(u2_t b) {
+  const uint32_t ex = 0x64646464u, a = b.x ^ 0x80808080u, c = b.y ^ 0x80808080u;
+  const h2_t m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  u4_t w;
+  w.x = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, a, 0x04020400u)) + m1152);
+  w.y = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, a, 0x04030401u)) + m1152);
+  w.z = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, c, 0x04020400u)) + m1152);
+  w.w = __builtin_bit_cast(uint32_t, as_h2(__builtin_amdgcn_perm(ex, c, 0x04030401u)) + m1152);
+  return __builtin_bit_cast(h8_t, w);
+}
+
 }  // namespace hy3x

@@ -238,9 +238,7 @@ int hy3x_layer_set_rms_scale(hy3x_layer *layer, const float *r, int n);
 /* Execution-path override for tests: 0 = automatic (by T), 1 = force the
  * wavefront-GEMV expert path, 2 = force the MFMA grouped-GEMM path (tile
  * shape by T), 3 = MFMA with the narrow tile shape (32 tokens), 4 = MFMA with
- * the wide tile shape (64 tokens), 5 = MFMA with 128-token tiles (Q4_K
- * shared expert only: a forward with a Q8_0 shared expert then fails with
- * HY3X_E_STATE). */
+ * the wide tile shape (64 tokens), 5 = MFMA with 128-token tiles. */
 int hy3x_layer_set_path(hy3x_layer *layer, int path);
 
 /* Which expert path the last forward ran: 0 = the fused single-token decode

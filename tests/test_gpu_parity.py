@@ -563,12 +563,13 @@ def test_q4k_shared_restored_after_q8(torch, layer, cpu):
     assert O.rel_l2(y - x, yo - x) <= TOL
 
 
-@pytest.mark.parametrize("T,path", [(2, 0), (40, 3), (40, 4), (64, 4)])
+@pytest.mark.parametrize("T,path", [(2, 0), (40, 3), (40, 4), (64, 4), (40, 5), (128, 5)])
 def test_q8_shared_mfma_matches_oracle(torch, q8_layer, cpu, q8_mats, T, path):
     """T >= 2 with hy3's Q8_0 shared expert: the MFMA grouped GEMM runs the
     shared expert's tiles from its Q8 matrices (T = 40, narrow shape: one tile
     of 32 tokens and one of 8; wide shape: one tile of 40, three 16-token
-    column groups; T = 64: one full wide tile)."""
+    column groups; T = 64: one full wide tile; 128-token tiles: one tile of 40,
+    one full tile of 128)."""
     x = O.normal(T * D, O.key(0xC1, 0, O.T_X), 1.0).reshape(T, D)
     q8_layer.set_path(path)
     try:
@@ -580,6 +581,27 @@ def test_q8_shared_mfma_matches_oracle(torch, q8_layer, cpu, q8_mats, T, path):
     assert O.rel_l2(y - x, yo - x) <= TOL
     for t in range(T):
         assert O.rel_l2(y[t] - x[t], yo[t] - x[t]) <= 2 * TOL, t
+
+
+@pytest.mark.parametrize("T", [40, 333, 2100])
+def test_q8_shared_big_tiles_equal_narrow_tiles(torch, q8_layer, T):
+    """With the Q8_0 shared expert the 128-token tiles run its tiles from the Q8
+    matrices with the narrow tiles' arithmetic: the same output bit for bit
+    (T = 2100 also runs them by default)."""
+    x = O.normal(T * D, O.key(0xC6, 0, O.T_X), 1.0).reshape(T, D)
+    try:
+        q8_layer.set_path(3)
+        y3 = run(torch, q8_layer, x)[0]
+        q8_layer.set_path(5)
+        y5 = run(torch, q8_layer, x)[0]
+        assert q8_layer.last_path() == 5
+        q8_layer.set_path(0)
+        y0 = run(torch, q8_layer, x)[0]
+        assert q8_layer.last_path() == (5 if T >= 2048 else 4 if T >= 384 else 3)
+    finally:
+        q8_layer.set_path(0)
+    assert np.array_equal(y3.view(np.uint32), y5.view(np.uint32))
+    assert np.array_equal(y3.view(np.uint32), y0.view(np.uint32))
 
 
 def test_q8_shared_reference_tokens(torch, q8_layer):
