@@ -171,23 +171,22 @@ __device__ __forceinline__ void big_step(State<GATEUP, NTT> &st, int s) {
       dequant_run(pv[rg][m].xy, ml, al, mh, ah, wf[rg][m][0], wf[rg][m][2]);
       dequant_run(pv[rg][m].zw, ml, al, mh, ah, wf[rg][m][1], wf[rg][m][3]);
     }
+  // k run outer, token groups inner: an MFMA's accumulator was last written
+  // 2 NTT MFMAs earlier, so the chains do not wait on each other
 #pragma unroll
-  for (int t = 0; t < NTT; t++) {
-    h8_t x[4];
+  for (int hu = 0; hu < 4; hu++) {
+    // chunk of k offset 32 hi + 8 u + 64 (g >> 1) + 16 (g & 1) within the half
+    const int c = 4 * ((hu >> 1) & 1) + (hu & 1) + gch;
 #pragma unroll
-    for (int hu = 0; hu < 4; hu++) {
-      // chunk of k offset 32 hi + 8 u + 64 (g >> 1) + 16 (g & 1) within the half
-      const int c = 4 * ((hu >> 1) & 1) + (hu & 1) + gch;
-      x[hu] = __builtin_bit_cast(h8_t, xs[16 * (16 * t + lr) + (c ^ lr)]);
-    }
-#pragma unroll
-    for (int hu = 0; hu < 4; hu++)
+    for (int t = 0; t < NTT; t++) {
+      const h8_t x = __builtin_bit_cast(h8_t, xs[16 * (16 * t + lr) + (c ^ lr)]);
 #pragma unroll
       for (int rg = 0; rg < RG; rg++)
 #pragma unroll
         for (int m = 0; m < NMAT; m++)
           st.dblk[rg][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              x[hu], wf[rg][m][hu], (h == 0 && hu == 0) ? zero4 : st.dblk[rg][m][t], 0, 0, 0);
+              x, wf[rg][m][hu], (h == 0 && hu == 0) ? zero4 : st.dblk[rg][m][t], 0, 0, 0);
+    }
   }
   if (h) {  // the column's mins MFMA, then acc += d * Dblk (the MFMA tiles' order)
 #pragma unroll
