@@ -118,9 +118,13 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
 // figures are recorded with the design notes, not as build switches).
 constexpr int DEC_RPW = 4;                   // gate/up rows per wave
 constexpr int DEC_GU_PF = 4;                 // gate/up rows in flight per wave
-constexpr int DEC_RPB = 4 * DEC_RPW;         // shared gate/up rows per routing block (four waves)
+// Shared gate/up rows per wave of a routing block: one, so that the shared
+// blocks (384 of 4 rows) finish before the router chains do (with 16-row
+// blocks the last ones ended about 1 us after the chains; C0 32.4 -> 31.5 us).
+constexpr int DEC_SH_RPW = 1;
+constexpr int DEC_RPB = 4 * DEC_SH_RPW;       // shared gate/up rows per routing block (four waves)
 static_assert(F % DEC_RPB == 0, "the routing kernel's shared blocks cover every row");
-constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (96)
+constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (384)
 // Waves per routed gate/up block (each block routes the token once, then its
 // waves stream DEC_RPW rows each).
 constexpr int DEC_GU_WAVES = 4;

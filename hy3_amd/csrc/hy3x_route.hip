@@ -119,8 +119,11 @@ __device__ __forceinline__ void router_block(
       score[(size_t)t * E + e] = has_bias ? sg + bias[e] : sg;
     }
     trace_point(trace, 3);
-  } else if (e == 0) {  // stage s for the expert kernels (fp16 pair-staged and fp32)
-    for (int j = tid - 8; j < D; j += 248) {
+  } else if (e == 0 && tid >= 64) {
+    // stage s for the expert kernels (fp16 pair-staged and fp32) from the
+    // waves that run no chain: lanes 8..63 of wave 0 would run it after the
+    // chain (one instruction stream), making block 0 the last router block
+    for (int j = tid - 64; j < D; j += 192) {
       const float sv = xsf[(j & 7) * RS + (j >> 3)];
       stage_store(s16 + (size_t)t * D, j, sv);
       s32[(size_t)t * D + j] = sv;
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(256) void k_route_decode(
     w4[u] = wg[tid + 256 * u];
   }
   const int lane = tid & 63, wave = tid >> 6, sb = blockIdx.x - E;
-  const int r0 = sb * DEC_RPB + wave * DEC_RPW;
+  const int r0 = sb * DEC_RPB + wave * DEC_SH_RPW;
   auto stage_s = [&](uint32_t (&X)[32], float &slo, float &shi) {
     if (xadd) {
 #pragma unroll
@@ -203,11 +206,11 @@ __global__ __launch_bounds__(256) void k_route_decode(
   uint32_t X[32];
   float slo, shi;
   if (wsh) {
-    GateupRowsQ8<DEC_RPW, 2> rows(wsh, K, r0);
+    GateupRowsQ8<DEC_SH_RPW, 2> rows(wsh, K, r0);
     stage_s(X, slo, shi);
     rows.finish(X, slo, shi, h16);
   } else {
-    GateupRows<DEC_RPW, DEC_RPW> rows(wq, E, K, r0);
+    GateupRows<DEC_SH_RPW, DEC_SH_RPW> rows(wq, E, K, r0);
     stage_s(X, slo, shi);
     rows.finish(X, slo, shi, h16);
   }
