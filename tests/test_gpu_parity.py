@@ -430,13 +430,14 @@ def test_big_tiles_equal_narrow_tiles(torch, layer, cpu, T):
     assert np.array_equal(y3.view(np.uint32), y5.view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [40, 200])
+@pytest.mark.parametrize("T", [40, 129, 200, 257])
 def test_mfma_tile_shapes_on_crowded_experts(torch, layer, cpu, T):
     """A bias of +50 on eight experts sends every token to them, so each of
     those experts holds all T tokens: the narrow shape (32-token tiles), the
     wide one (64-token tiles: T = 40 is one tile of 40 tokens, three 16-token
     column groups; T = 200 is three full tiles of four groups and one of 8
-    tokens) and the 128-token tiles give the same output bit for bit (the same per-element arithmetic
+    tokens) and the 128-token tiles (T = 129 and 257: full tiles plus a tile of
+    one token) give the same output bit for bit (the same per-element arithmetic
     in every 16-token group and either shape), within the tolerance of the
     oracle's."""
     nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
