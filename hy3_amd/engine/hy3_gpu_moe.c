@@ -116,8 +116,11 @@ int hy3_gpu_init(hy3_model *m, int n_gpu_layers) {
     if (check_layer(&m->w.layers[il], il)) return -1;
   moe_ctx *c = (moe_ctx *)calloc(1, sizeof(moe_ctx));
   if (!c) return -1;
+  // tokens per forward: a whole long prompt per call where it fits (from 2048
+  // tokens the library runs its 128-token tiles: one 4096-token forward takes
+  // about 2.5 ms against 8 x 0.65 ms in 512-token chunks)
   const char *chunk = getenv("HY3_PREFILL_CHUNK");
-  c->max_tokens = (chunk && atoi(chunk) > 0) ? atoi(chunk) : 512;
+  c->max_tokens = (chunk && atoi(chunk) > 0) ? atoi(chunk) : 4096;
   c->n_layers = n_gpu_layers;
   hy3x_layer *first = NULL;
   for (int il = HY3_N_LAYER_DENSE; il < n_gpu_layers; il++) {

@@ -50,7 +50,7 @@ void hy3_gpu_free(hy3_model *m);
  * [T x 4096] fp32) += shared(s) + sum_k w_k expert_k(s), s = rmsnorm(x) *
  * ffn_norm, with K = m->n_expert_used (clamped to [1, 8]) and the 2.826
  * route scale (hy3.c:1266-1325). Any T >= 1: tokens beyond the forward's
- * capacity (HY3_PREFILL_CHUNK at init, else 512) run in consecutive chunks.
+ * capacity (HY3_PREFILL_CHUNK at init, else 4096) run in consecutive chunks.
  * stream: a hipStream_t, or NULL. Asynchronous. 0, or -1 when there is no
  * context, il is not a bound MoE layer, or a HIP call fails. */
 int hy3_gpu_ffn_moe(hy3_model *m, int il, float *x, int T, void *stream);

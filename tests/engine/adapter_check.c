@@ -279,7 +279,7 @@ static int run(void) {
   CHECK(hy3_gpu_init(m, 0) == -1 && m->gpu_ctx == NULL,
         "hy3_gpu_init(m, 0) means 81 layers: layer 3 has no MoE tensors, refused");
   CHECK(hy3_gpu_init(m, 2) == 0 && m->gpu_layers == 2, "hy3_gpu_init(m, 2) again after free");
-  compare(m, &src[1], 1, 600, 8, 512, 0xE6); /* default chunk 512 */
+  compare(m, &src[1], 1, 600, 8, 4096, 0xE6); /* default chunk 4096: one forward */
   hy3_gpu_free(m);
   for (int il = 1; il <= 2; il++) hy3x_layer_destroy(src[il].direct);
   free(m);
