@@ -133,5 +133,11 @@ static_assert(F % DEC_GU_RPB == 0, "whole blocks per expert");
 constexpr int DEC_GU_BLOCKS = F / DEC_GU_RPB;       // routed gate/up blocks per expert
 constexpr int DEC_DOWN_RPB = 16;  // down rows per block
 constexpr int DEC_DOWN_PF = 2;    // down passes (2 rows each) in flight per wave
+// Waves of a down block: one per routed slot, then the shared expert's rows
+// split over DEC_DOWN_SH_WAVES waves, so that every SIMD runs the same number
+// of passes (with one shared wave, the SIMD holding three waves set the pace).
+constexpr int DEC_DOWN_SH_WAVES = 4;
+constexpr int DEC_DOWN_WAVES = KMAX + DEC_DOWN_SH_WAVES;
+static_assert(DEC_DOWN_RPB % (2 * DEC_DOWN_SH_WAVES) == 0, "whole passes per shared wave");
 
 }  // namespace hy3x

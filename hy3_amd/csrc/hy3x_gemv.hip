@@ -239,8 +239,9 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
 
 // Down of a single token for rows blockIdx.x*RPB .. +RPB, fused with the
 // combine y = x + (shared + sum_k w_k * down_k), k in selection order
-// (hy3.c:1302, 1318-1319, 1324-1325). Wave k owns slot k (k < K routed,
-// k = K the shared expert): its passes of 2 rows stream through a register
+// (hy3.c:1302, 1318-1319, 1324-1325). Wave k < K owns routed slot k, waves
+// KMAX .. KMAX + 3 a quarter of the rows each of the shared expert (waves
+// K .. KMAX - 1 are idle): their passes of 2 rows stream through a register
 // ring of DEC_DOWN_PF passes (down_rows; 2 measured best), the row sums go
 // to LDS, and DEC_DOWN_RPB threads combine them. wsh != nullptr: the shared
 // expert is the layer's Q8 one (down_rows_q8). A variant that copied each
@@ -248,26 +249,37 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
 // in back-to-back replays of this kernel alone but slower inside the
 // forward (decode 32.9 vs 32.1 us, 79-layer stack 2.87 vs 2.82 ms): its
 // 157 KB of LDS per block keeps a block off a CU until the CU is empty.
-__global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
+__global__ __launch_bounds__(64 * DEC_DOWN_WAVES) void k_down_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
     const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
     float *__restrict__ x, const float *__restrict__ xadd, const uint8_t *__restrict__ wsh,
     unsigned long long *trace) {
-  constexpr int RPB = DEC_DOWN_RPB;
-  __shared__ float out_l[KMAX + 1][RPB];
+  constexpr int RPB = DEC_DOWN_RPB, SH_ROWS = RPB / DEC_DOWN_SH_WAVES;
+  __shared__ float out_l[KMAX + 1][RPB];  // [KMAX]: the shared expert
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int r0 = blockIdx.x * RPB;
-  auto keep = [&](int ps, float2 t) {
-    if (lane == 0) {
-      out_l[k][2 * ps] = t.x;
-      out_l[k][2 * ps + 1] = t.y;
-    }
-  };
-  if (k == K && wsh)
-    down_rows_q8<RPB / 2, DEC_DOWN_PF>(wsh, h16 + (size_t)K * F, r0, keep);
-  else if (k <= K)
-    down_rows<RPB / 2, DEC_DOWN_PF>(wq, k < K ? ids[k] : E, h16 + (size_t)k * F, r0, keep);
+  if (k >= KMAX) {  // a quarter of the block's rows of the shared expert
+    const int q = k - KMAX;
+    auto keep = [&](int ps, float2 t) {
+      if (lane == 0) {
+        out_l[KMAX][q * SH_ROWS + 2 * ps] = t.x;
+        out_l[KMAX][q * SH_ROWS + 2 * ps + 1] = t.y;
+      }
+    };
+    if (wsh)
+      down_rows_q8<SH_ROWS / 2, DEC_DOWN_PF>(wsh, h16 + (size_t)K * F, r0 + q * SH_ROWS, keep);
+    else
+      down_rows<SH_ROWS / 2, DEC_DOWN_PF>(wq, E, h16 + (size_t)K * F, r0 + q * SH_ROWS, keep);
+  } else if (k < K) {
+    auto keep = [&](int ps, float2 t) {
+      if (lane == 0) {
+        out_l[k][2 * ps] = t.x;
+        out_l[k][2 * ps + 1] = t.y;
+      }
+    };
+    down_rows<RPB / 2, DEC_DOWN_PF>(wq, ids[k], h16 + (size_t)k * F, r0, keep);
+  }
   __syncthreads();
   trace_point(trace, 2);
   if (threadIdx.x < RPB) {
@@ -275,7 +287,7 @@ __global__ __launch_bounds__(64 * (KMAX + 1)) void k_down_decode(
     float eo = 0.0f;
     for (int kk = 0; kk < K; kk++) eo = __builtin_fmaf(w[kk], out_l[kk][threadIdx.x], eo);
     const float xr = xadd ? x[r] + xadd[r] : x[r];
-    x[r] = xr + (out_l[K][threadIdx.x] + eo);
+    x[r] = xr + (out_l[KMAX][threadIdx.x] + eo);
   }
   trace_point(trace, 3);
 }

@@ -556,7 +556,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
-        k_down_decode<<<D / DEC_DOWN_RPB, 64 * (KMAX + 1), 0, st>>>(
+        k_down_decode<<<D / DEC_DOWN_RPB, 64 * DEC_DOWN_WAVES, 0, st>>>(
             L->wq, S.h16, S.ids, S.w, K, x, c.xadd, L->shared_q8 ? L->wsh : nullptr,
             L->trace[2]);
       else if (c.mode == Mode::MFMA) {
