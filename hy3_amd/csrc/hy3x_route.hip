@@ -48,20 +48,33 @@ __device__ __forceinline__ void load_transposed(const float *src, float *buf, in
   }
 }
 
-// One fmaf chain over a chain-transposed row pair (512 steps, i ascending).
-// (A variant double-buffering 32-step chunks in registers measured slower:
-// it doubled the kernel's registers and halved its occupancy.)
-__device__ __forceinline__ float chain_dot(const float *a, const float *b) {
-  const float4 *av = reinterpret_cast<const float4 *>(a);
-  const float4 *bv = reinterpret_cast<const float4 *>(b);
+// The eight fmaf chains of one logit over chain-transposed row pairs (512
+// steps each, i ascending), with their operands in registers spread over a
+// whole wave: lane 8 g + v holds steps [64 g, 64 g + 64) of chain v (64
+// router and 64 s values). The wave runs 8 rounds of 64 FMAs; in round g the
+// lanes of segment g continue chain v from the accumulator the lanes of
+// segment g - 1 left (moved up 8 lanes between rounds); the other lanes'
+// results are discarded. The chain is bound by the dependent FMA latency, and
+// no FMA waits on LDS (8 lanes each running a whole chain from LDS took about
+// 1.5 times as long). Returns chain v's total in lane 56 + v.
+__device__ __forceinline__ float chain_lanes(const float *rs, const float *xs, int lane) {
+  const int v = lane & 7, seg = lane >> 3;
+  float a[64], b[64];
+  const float4 *av = reinterpret_cast<const float4 *>(rs + v * RS + 64 * seg);
+  const float4 *bv = reinterpret_cast<const float4 *>(xs + v * RS + 64 * seg);
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const float4 p = av[j], q = bv[j];
+    a[4 * j] = p.x; a[4 * j + 1] = p.y; a[4 * j + 2] = p.z; a[4 * j + 3] = p.w;
+    b[4 * j] = q.x; b[4 * j + 1] = q.y; b[4 * j + 2] = q.z; b[4 * j + 3] = q.w;
+  }
   float acc = 0.0f;
-#pragma unroll 16
-  for (int q = 0; q < NI / 4; q++) {
-    const float4 x = av[q], y = bv[q];
-    acc = __builtin_fmaf(x.x, y.x, acc);
-    acc = __builtin_fmaf(x.y, y.y, acc);
-    acc = __builtin_fmaf(x.z, y.z, acc);
-    acc = __builtin_fmaf(x.w, y.w, acc);
+#pragma unroll 1
+  for (int g = 0; g < 8; g++) {
+#pragma unroll
+    for (int j = 0; j < 64; j++) acc = __builtin_fmaf(a[j], b[j], acc);
+    const float up = __shfl_up(acc, 8, 64);
+    if (seg == g + 1) acc = up;
   }
   return acc;
 }
@@ -69,8 +82,8 @@ __device__ __forceinline__ float chain_dot(const float *a, const float *b) {
 // ---------------------------------------------------------------------------
 // Small T: one block per (expert, token). The block stages x, norm_w and the
 // router row in LDS transposed by chain (buf[v][i] = a[8i+v]), reduces the
-// sum of squares in the fixed block order, then lanes 0..7 run the eight
-// logit chains. Block (0, t) also stages s for the expert kernels.
+// sum of squares in the fixed block order, then wave 0 runs the eight logit
+// chains (chain_lanes). Block (0, t) also stages s for the expert kernels.
 __device__ __forceinline__ void router_block(
     int e, int t, const float *__restrict__ x, const float *__restrict__ xadd,
     const float *__restrict__ norm_w, const float *__restrict__ router,
@@ -110,9 +123,9 @@ __device__ __forceinline__ void router_block(
   const float r = r_blk;
   for (int q = tid; q < 8 * RS; q += 256) xsf[q] = (xsf[q] * wsf[q]) * r;  // s, in place
   __syncthreads();
-  if (tid < 8) {  // logit chain `tid`
-    const float lg = tree8_lanes(chain_dot(rsf + tid * RS, xsf + tid * RS), tid);
-    if (tid == 0) {
+  if (tid < 64) {  // the eight logit chains in wave 0
+    const float lg = tree8_lanes(chain_lanes(rsf, xsf, tid), tid & 7);
+    if (tid == 56) {
       const float sg = sigmoid_c(lg);
       logits[(size_t)t * E + e] = lg;
       sig[(size_t)t * E + e] = sg;
@@ -121,8 +134,7 @@ __device__ __forceinline__ void router_block(
     trace_point(trace, 3);
   } else if (e == 0 && tid >= 64) {
     // stage s for the expert kernels (fp16 pair-staged and fp32) from the
-    // waves that run no chain: lanes 8..63 of wave 0 would run it after the
-    // chain (one instruction stream), making block 0 the last router block
+    // waves that run no chain
     for (int j = tid - 64; j < D; j += 192) {
       const float sv = xsf[(j & 7) * RS + (j >> 3)];
       stage_store(s16 + (size_t)t * D, j, sv);
