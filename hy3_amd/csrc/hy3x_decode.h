@@ -117,7 +117,7 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
 // Decode launch shapes (measured on MI355X; the alternatives tried and their
 // figures are recorded with the design notes, not as build switches).
 constexpr int DEC_RPW = 4;                   // gate/up rows per wave
-constexpr int DEC_GU_PF = 4;                 // gate/up rows in flight per wave
+constexpr int DEC_GU_PF = 2;                 // gate/up rows in flight per wave (4: all of them, 0.3-0.4 us slower)
 // Shared gate/up rows per wave of a routing block: one, so that the shared
 // blocks (384 of 4 rows) finish before the router chains do (with 16-row
 // blocks the last ones ended about 1 us after the chains; C0 32.4 -> 31.5 us).
