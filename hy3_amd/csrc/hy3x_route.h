@@ -99,11 +99,11 @@ __device__ __forceinline__ void wave_best(float &v, int &key) {
   key = bk;
 }
 
-// Top-K of one token by one wave (hy3.c:1282-1291). Expert e sits at lane
-// e % 64, slot e / 64 of sc (biased score) and sg (sigmoid). Selection with
-// swaps: step k takes the largest score among positions >= k, ties to the
-// lowest current position, and the element at position k moves to the
-// winner's position. Then sum = sigma_sel0 + sigma_sel1 + ... in selection
+// Top-K of one token by one wave (hy3.c:654-666, 1282-1291). Expert e sits
+// at lane e % 64, slot e / 64 of sc (biased score) and sg (sigmoid). Selection
+// with swaps: step k takes the largest score among positions >= k, ties to
+// the lowest current position, a NaN at position k kept, NaNs elsewhere
+// never taken; the element at position k moves to the winner's position. Then sum = sigma_sel0 + sigma_sel1 + ... in selection
 // order, inv = 1 / (sum + 1e-20), wpre_k = sigma_k * inv, w_k = wpre_k * scale.
 // Everything stays in registers; lane k < K writes ids[k], wpre[k], wout[k].
 __device__ __forceinline__ void topk_wave_regs(const float (&sc)[3], const float (&sg)[3], int K,
@@ -120,8 +120,14 @@ __device__ __forceinline__ void topk_wave_regs(const float (&sc)[3], const float
 #pragma unroll
     for (int m = 0; m < 3; m++) {
       const int key = pos[m] * 256 + lane + 64 * m;
-      if (pos[m] >= k && (sc[m] > bv || (sc[m] == bv && key < bk))) {
-        bv = sc[m];
+      // the scan starts from the element at position k and only a strictly
+      // greater score replaces it: a NaN there is never replaced (+inf wins
+      // every tie by its lowest position), a NaN elsewhere never wins (it
+      // compares false). Position k is always a candidate, so some element
+      // always wins.
+      const float v = (pos[m] == k && sc[m] != sc[m]) ? __builtin_huge_valf() : sc[m];
+      if (pos[m] >= k && (v > bv || (v == bv && key < bk))) {
+        bv = v;
         bk = key;
       }
     }

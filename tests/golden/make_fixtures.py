@@ -9,6 +9,7 @@ Runs ONLY in a container that holds the reference sources at /root/reference
   q4k_quant.npz     hy3_convert.c quantize_row_q4_K (:605-651) on edge + random blocks
   q4k_dequant.npz   hy3.c dequantize_row_q4_K (:1019-1043) on those blocks + special headers
   topk.npz          hy3.c topk_select (:654-666) on tie-heavy score vectors
+  topk_nonfinite.npz  the same on score vectors holding NaN and +-inf
   layer.json        SHA-256 of every expert matrix of the synthetic layer (seed 0xC0,
                     layer 0) quantised by the reference quantiser, and of the small tensors
   moe.npz           hy3.c forward_layer_moe (:1219-1326) on config tokens: router scores
@@ -26,7 +27,7 @@ Runs ONLY in a container that holds the reference sources at /root/reference
                     expert) at small shapes: the GGUF framing the writer and the library's
                     loader are checked against
 
-Usage: python tests/golden/make_fixtures.py [--only q8|gguf]   (all: about 2 minutes on 8 cores)
+Usage: python tests/golden/make_fixtures.py [--only q8|gguf|topk]   (all: about 2 minutes on 8 cores)
 """
 import argparse
 import hashlib
@@ -130,9 +131,38 @@ def gguf_fixture(R):
     print("gguf fixture written", flush=True)
 
 
+def topk_nonfinite(R):
+    """topk_nonfinite.npz: hy3.c topk_select (:654-666) on score vectors with
+    NaN and +-inf entries (a NaN at the scan's first position is kept, a NaN
+    elsewhere never wins)."""
+    rng = np.random.default_rng(654)
+    base = rng.standard_normal(192).astype(np.float32)
+    sets = []
+    s = np.full(192, np.nan, np.float32); sets.append(s)
+    for where in (0, 1, 5, 7, 8, 191, int(np.argmax(base))):
+        s = base.copy(); s[where] = np.nan; sets.append(s)
+    s = base.copy(); s[::3] = np.nan; sets.append(s)
+    s = base.copy(); s[1::2] = np.nan; sets.append(s)
+    s = base.copy(); s[7] = np.inf; s[9] = -np.inf; s[100] = np.inf; sets.append(s)
+    s = np.full(192, -np.inf, np.float32); sets.append(s)
+    s = np.full(192, -np.inf, np.float32); s[50] = np.nan; s[2] = 0.0; sets.append(s)
+    s = np.full(192, np.inf, np.float32); s[3] = np.nan; sets.append(s)
+    s = np.full(192, np.nan, np.float32); s[[10, 70, 130]] = 1.0; sets.append(s)
+    scores = np.stack(sets)
+    vals = np.zeros((len(sets), 8, 8), np.float32)
+    inds = np.full((len(sets), 8, 8), -1, np.int32)
+    for i, sc in enumerate(scores):
+        for k in range(1, 9):
+            v = np.zeros(k, np.float32); ix = np.zeros(k, np.int32)
+            R.hy3ref_topk_select(v.ctypes.data, ix.ctypes.data, sc.ctypes.data, 192, k)
+            vals[i, k - 1, :k] = v; inds[i, k - 1, :k] = ix
+    np.savez_compressed(os.path.join(OUT, "topk_nonfinite.npz"), scores=scores, vals=vals,
+                        inds=inds)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", choices=["q8", "gguf"], default=None)
+    ap.add_argument("--only", choices=["q8", "gguf", "topk"], default=None)
     a = ap.parse_args()
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref", f"REF={REF}"],
                    check=True)
@@ -143,6 +173,9 @@ def main():
         return
     if a.only == "gguf":
         gguf_fixture(R)
+        return
+    if a.only == "topk":
+        topk_nonfinite(R)
         return
     meta = {
         "reference": REF,
@@ -231,6 +264,7 @@ def main():
             R.hy3ref_topk_select(v.ctypes.data, ix.ctypes.data, sc.ctypes.data, 192, k)
             vals[i, k - 1, :k] = v; inds[i, k - 1, :k] = ix
     np.savez_compressed(os.path.join(OUT, "topk.npz"), scores=scores, vals=vals, inds=inds)
+    topk_nonfinite(R)
     print("unit fixtures done", flush=True)
 
     # the synthetic layer, quantised by the reference quantiser

@@ -411,6 +411,64 @@ def test_expert_paths_match_oracle(torch, layer, cpu, T):
         layer.set_path(0)
 
 
+@pytest.mark.parametrize("T,bad", [(1, np.nan), (3, np.nan), (40, np.nan), (40, np.inf)])
+def test_non_finite_token(torch, layer, cpu, T, bad):
+    """A token with a NaN or an infinity in x: its scores are NaN, and the
+    selection with strict '>' (hy3.c:654-666) then keeps the experts in
+    position order -- the routing equals the oracle's, with NaN gate weights
+    and a NaN output row; every other token of the batch is bit for bit what
+    it is without the bad token (decode path at T = 1, tiles otherwise)."""
+    x = C.inputs(0xC8, T)
+    bt = T // 2
+    xb = x.copy()
+    xb[bt, 5] = bad
+    y, ids, wpre, w = run(torch, layer, xb)
+    r = cpu.route(xb)
+    assert np.array_equal(ids, r["ids"])
+    assert np.isnan(wpre[bt]).all() and np.isnan(r["wpre"][bt]).all()
+    ok = np.arange(T) != bt
+    assert np.array_equal(wpre[ok].view(np.uint32), r["wpre"][ok].view(np.uint32))
+    assert np.isnan(y[bt]).all()
+    if T > 1:
+        y0 = run(torch, layer, x)[0]
+        assert np.array_equal(y[ok].view(np.uint32), y0[ok].view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 2, 40, 300])
+def test_non_finite_bias(torch, layer, cpu, T):
+    """NaN and infinite router biases make some experts' scores non-finite
+    while their sigmoids stay finite: a NaN taken at the scan's first position
+    (experts 0 and 3 sit at the first positions) stays selected, NaNs
+    elsewhere never win, +inf experts come first and -inf ones never (hy3.c
+    :654-666). Routing equals the oracle's bit for bit, on every path, and the
+    output is within the oracle's tolerance."""
+    nw, rt, b0 = C.layer_small_tensors(C.WEIGHT_SEED)
+    b = b0.copy()
+    b[[0, 3, 64, 100, 150, 191]] = np.nan
+    b[[7, 120]] = np.inf
+    b[[1, 2, 5]] = -np.inf
+    layer.set_router(nw, rt, b)
+    saved = cpu.bias
+    cpu.bias = b
+    x = C.inputs(0xC9, T)
+    try:
+        r = cpu.route(x)
+        assert set(r["ids"][:, :2].ravel().tolist()) <= {0, 7, 120}
+        for path in ((0,) if T == 1 else (0, 3, 4, 5)):
+            layer.set_path(path)
+            y, ids, wpre, _ = run(torch, layer, x)
+            assert np.array_equal(ids, r["ids"]), path
+            assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32)), path
+            assert np.isfinite(y).all()
+        rows = np.linspace(0, T - 1, min(T, 4)).astype(int)
+        yo, _ = cpu.forward(x[rows])
+        assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL
+    finally:
+        layer.set_path(0)
+        layer.set_router(nw, rt, b0)
+        cpu.bias = saved
+
+
 @pytest.mark.parametrize("T", [2, 40, 333, 1000, 4096])
 def test_big_tiles_equal_narrow_tiles(torch, layer, cpu, T):
     """The 128-token tiles (activations staged per half block column, the

@@ -107,6 +107,16 @@ def test_topk_matches_reference():
             assert np.array_equal(v.view(np.uint32), f["vals"][i, k - 1, :k].view(np.uint32))
 
 
+def test_topk_nonfinite_matches_reference():
+    # NaN / inf scores: a NaN at the scan's first position stays, others never win
+    f = load("topk_nonfinite.npz")
+    for i, sc in enumerate(f["scores"]):
+        for k in range(1, 9):
+            v, ix = O.topk_select(sc, k)
+            assert np.array_equal(ix, f["inds"][i, k - 1, :k]), (i, k)
+            assert np.array_equal(v.view(np.uint32), f["vals"][i, k - 1, :k].view(np.uint32))
+
+
 def test_topk_invariants():
     rng = np.random.default_rng(5)
     for _ in range(50):
