@@ -72,8 +72,8 @@ __device__ __forceinline__ void gateup_rows(const uint8_t *__restrict__ wq, int 
 // PF passes in flight, and fn(ps, sums) gets the two row sums of pass ps
 // (row r0 + 2 ps in .x, r0 + 2 ps + 1 in .y, wave-uniform). h: the slot's
 // staged h (hy3.c:1316-1317).
-template <int PASSES, int PF, typename Fn>
-__device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
+template <int PASSES, int PF, typename Expert, typename Fn>
+__device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, Expert &&expert,
                                           const __half *__restrict__ h, int r0, Fn &&fn) {
   constexpr int G = F / 64;
   const int lane = threadIdx.x & 63, hw = lane >> 5, gl = lane & 31;
@@ -84,6 +84,14 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
   const int glc = active ? gl : G - 1;
   const int b = glc >> 2, p = glc & 3;
   const ScaleSel sel(p);
+  // h first: loads complete in issue order for the wait counters, so h
+  // issued after the weight ring would hold the first pass back until the
+  // whole ring had landed. The expert id (expert(): a constant, or a load
+  // from memory) is read after h's loads are in flight.
+  uint32_t X[32];
+  load_group_x(h, glc, X);
+  asm volatile("" ::: "memory");  // h's loads issue before the id's
+  const int e = expert();
   const uint8_t *dbase = wq + (size_t)e * EXPERT_BYTES + 2 * MAT_BYTES + (size_t)b * QB;
   uint4 ring[PF][3];
   auto issue = [&](int ps, uint4 (&dst)[3]) {
@@ -92,11 +100,6 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, int e,
     dst[1] = *reinterpret_cast<const uint4 *>(dp + 16 + 32 * p);
     dst[2] = *reinterpret_cast<const uint4 *>(dp + 32 + 32 * p);
   };
-  // h first: loads complete in issue order for the wait counters, so h
-  // issued after the weight ring would hold the first pass back until the
-  // whole ring had landed
-  uint32_t X[32];
-  load_group_x(h, glc, X);
 #pragma unroll
   for (int ps = 0; ps < PF && ps < PASSES; ps++) issue(ps, ring[ps]);
   float slo = 0.0f, shi = 0.0f;

@@ -259,6 +259,16 @@ __global__ __launch_bounds__(64 * DEC_DOWN_WAVES) void k_down_decode(
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int r0 = blockIdx.x * RPB;
+  // the combine's inputs (residual row, gate weights), loaded before the
+  // weight streams so that they are in registers when the row sums are
+  // (raw values: an add here would wait for the loads)
+  float xv = 0.0f, xav = 0.0f, wv = 0.0f;
+  if (k == 0) {
+    const int r = r0 + (lane < RPB ? lane : 0);
+    xv = x[r];
+    if (xadd) xav = xadd[r];
+    wv = w[lane < K ? lane : 0];  // lane kk holds w[kk]
+  }
   if (k >= KMAX) {  // a quarter of the block's rows of the shared expert
     const int q = k - KMAX;
     auto keep = [&](int ps, float2 t) {
@@ -270,7 +280,8 @@ __global__ __launch_bounds__(64 * DEC_DOWN_WAVES) void k_down_decode(
     if (wsh)
       down_rows_q8<SH_ROWS / 2, DEC_DOWN_PF>(wsh, h16 + (size_t)K * F, r0 + q * SH_ROWS, keep);
     else
-      down_rows<SH_ROWS / 2, DEC_DOWN_PF>(wq, E, h16 + (size_t)K * F, r0 + q * SH_ROWS, keep);
+      down_rows<SH_ROWS / 2, DEC_DOWN_PF>(wq, [] { return E; }, h16 + (size_t)K * F,
+                                          r0 + q * SH_ROWS, keep);
   } else if (k < K) {
     auto keep = [&](int ps, float2 t) {
       if (lane == 0) {
@@ -278,15 +289,19 @@ __global__ __launch_bounds__(64 * DEC_DOWN_WAVES) void k_down_decode(
         out_l[k][2 * ps + 1] = t.y;
       }
     };
-    down_rows<RPB / 2, DEC_DOWN_PF>(wq, ids[k], h16 + (size_t)k * F, r0, keep);
+    const int ku = __builtin_amdgcn_readfirstlane(k);  // a scalar load of the id
+    down_rows<RPB / 2, DEC_DOWN_PF>(wq, [&] { return ids[ku]; }, h16 + (size_t)k * F, r0, keep);
   }
   __syncthreads();
   trace_point(trace, 2);
   if (threadIdx.x < RPB) {
     const int r = r0 + threadIdx.x;
     float eo = 0.0f;
-    for (int kk = 0; kk < K; kk++) eo = __builtin_fmaf(w[kk], out_l[kk][threadIdx.x], eo);
-    const float xr = xadd ? x[r] + xadd[r] : x[r];
+    for (int kk = 0; kk < K; kk++)
+      eo = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                              __builtin_bit_cast(int, wv), kk)),
+                          out_l[kk][threadIdx.x], eo);
+    const float xr = xadd ? xv + xav : xv;
     x[r] = xr + (out_l[KMAX][threadIdx.x] + eo);
   }
   trace_point(trace, 3);

@@ -92,6 +92,47 @@ struct MfmaCfg {
   static_assert(TROWS * NMAT == RB, "row-blocks per tile");
 };
 
+// Weight copy schedule. OWN_COPIES (the wide shape): each wave copies
+// exactly the row-blocks it reads, so it needs no barrier for its weights
+// and issues column kb + 1 into the stage its own reads of kb - 1 used
+// before it waits for kb -- two weight columns in flight (measured: 512
+// tokens 643 -> 633 us; the narrow shape, two workgroups per CU, 290 -> 298
+// us at 32 tokens, so it keeps the split copies issued after the barrier).
+#ifdef HY3X_MFMA_WIDE
+constexpr bool OWN_COPIES = true;
+#else
+constexpr bool OWN_COPIES = false;
+#endif
+// LDS position (row-block index) of the lane's row-block of 16-row group rg,
+// matrix m. OWN_COPIES: each wave's own row-blocks are contiguous (wave, then
+// matrix, then group); otherwise gate rows, then up rows, in row order.
+template <bool GATEUP>
+__device__ __forceinline__ int rb_pos(int wave, int m, int rg, int lr) {
+  using C = MfmaCfg<GATEUP>;
+  if (!OWN_COPIES) return (GATEUP ? m * RB_HALF : 0) + 16 * (C::RG * wave + rg) + lr;
+  return 16 * (C::RG * C::NMAT * wave + C::RG * m + rg) + lr;
+}
+// Byte offset, within an expert's (or the shared expert's) matrices of stride
+// mat_bytes, of local weight chunk cl (< A_CHUNKS_WAVE) of this wave's copy
+// of a column: LDS chunk A_CHUNKS_WAVE * wave + cl = row-block (in rb_pos
+// order) / 9, 16-byte piece % 9.
+template <bool GATEUP>
+__device__ __forceinline__ uint32_t a_src(int wave, int cl, int rt, int64_t mat_bytes, int nkb) {
+  using C = MfmaCfg<GATEUP>;
+  if (!OWN_COPIES) {
+    int c = A_CHUNKS_WAVE * wave + cl;
+    if (c >= A_CHUNKS) c = A_CHUNKS - 1;
+    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
+    const int m = GATEUP ? rb / RB_HALF : 2, lrow = GATEUP ? rb % RB_HALF : rb;
+    return (uint32_t)(m * mat_bytes + (int64_t)(rt * C::TROWS + lrow) * nkb * QB + 16 * pc);
+  }
+  if (cl >= A_CHUNKS_WAVE) cl = A_CHUNKS_WAVE - 1;  // inactive lanes of the last copy
+  const int j = cl / RB_CHUNKS, pc = cl % RB_CHUNKS;
+  const int m = GATEUP ? j / (16 * C::RG) : 2, jr = j % (16 * C::RG);
+  const int row = rt * C::TROWS + 16 * C::RG * wave + jr;
+  return (uint32_t)(m * mat_bytes + (int64_t)row * nkb * QB + 16 * pc);
+}
+
 // Copy sources of one work tile: wave-uniform bases (scalar registers) plus
 // per-lane byte offsets, so that a copy costs no vector instruction. Column
 // kb adds kb blocks to the bases.
@@ -177,9 +218,18 @@ __device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
   // kb + 1 .. kb + A_AHEAD - 1, the last copies issued, may be in flight) and
   // its reads of kb - 1 are done; after the barrier the same holds for every
   // wave
-  wait_copies_and_barrier<VM_IN_FLIGHT>();
-  issue_b(st, kb + 1 < NKB ? kb + 1 : NKB - 1);  // past the end: a harmless re-copy
-  issue_a(st, kb + A_AHEAD < NKB ? kb + A_AHEAD : NKB - 1);
+  if (OWN_COPIES) {
+    // this wave's weights of kb + 1 go into the stage its own reads of kb - 1
+    // used (a wave reads only the row-blocks it copies), before the wait: two
+    // weight columns in flight
+    issue_a(st, kb + 1 < NKB ? kb + 1 : NKB - 1);  // past the end: a harmless re-copy
+    wait_copies_and_barrier<A_DMA>();
+    issue_b(st, kb + 1 < NKB ? kb + 1 : NKB - 1);
+  } else {
+    wait_copies_and_barrier<VM_IN_FLIGHT>();
+    issue_b(st, kb + 1 < NKB ? kb + 1 : NKB - 1);  // past the end: a harmless re-copy
+    issue_a(st, kb + A_AHEAD < NKB ? kb + A_AHEAD : NKB - 1);
+  }
 
   const u4_t *as = &a_ring[kb % A_STAGES][0];
   // byte selector of this lane group's sub-block pairs, activation chunk offset
@@ -196,7 +246,7 @@ __device__ __forceinline__ void mfma_step(TileState<GATEUP, NTT> &st, int kb) {
   for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
-      const int rb = (GATEUP ? m * RB_HALF : 0) + 16 * (RG * wave + rg) + lr;
+      const int rb = rb_pos<GATEUP>(wave, m, rg, lr);
       hdr[rg][m] = as[rb * RB_CHUNKS];
       pv[rg][m][0] = as[rb * RB_CHUNKS + 1 + g];
       pv[rg][m][1] = as[rb * RB_CHUNKS + 5 + g];
@@ -309,17 +359,12 @@ __device__ __forceinline__ void mfma_tile(const uint8_t *__restrict__ wq,
   const int lr = lane & 15, g = lane >> 4;
   TileState<GATEUP, NTT> st;
 
-  // weights: wave w copies chunks [288 w, 288 w + 288) of the column's
-  // (row-block c / 9, 16-byte piece c % 9), 64 per copy
+  // weights: wave w copies LDS chunks [288 w, 288 w + 288) of the column
+  // (row-block c / 9 in rb_pos order, 16-byte piece c % 9), 64 per copy
   st.abase = wq + (size_t)__builtin_amdgcn_readfirstlane(e) * EXPERT_BYTES;
 #pragma unroll
-  for (int j = 0; j < A_DMA; j++) {
-    int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
-    if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
-    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
-    const int m = GATEUP ? rb / RB_HALF : 2, lrow = GATEUP ? rb % RB_HALF : rb;
-    st.aoff[j] = (uint32_t)(m * MAT_BYTES + (rt * C::TROWS + lrow) * NKB * QB + 16 * pc);
-  }
+  for (int j = 0; j < A_DMA; j++)
+    st.aoff[j] = a_src<GATEUP>(wave, 64 * j + lane, rt, MAT_BYTES, NKB);
   st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
   // activations: copy j of wave w fills positions q = 64 (B_DMA w + j) + lane
   // of the 32 x 32 chunk tile: row r = q / 32, position q % 32 holds chunk
@@ -408,9 +453,15 @@ __device__ __forceinline__ void mfma_step_q8(TileStateQ8<GATEUP, NTT> &st, int k
   constexpr int RG = S::RG, NMAT = S::NMAT, NKB = S::NKB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, g = lane >> 4;
-  wait_copies_and_barrier<VM_IN_FLIGHT>();
-  issue_b_q8(st, kb + 1 < NKB ? kb + 1 : NKB - 1);
-  issue_a(st, kb + A_AHEAD < NKB ? kb + A_AHEAD : NKB - 1);
+  if (OWN_COPIES) {  // as mfma_step
+    issue_a(st, kb + 1 < NKB ? kb + 1 : NKB - 1);
+    wait_copies_and_barrier<A_DMA>();
+    issue_b_q8(st, kb + 1 < NKB ? kb + 1 : NKB - 1);
+  } else {
+    wait_copies_and_barrier<VM_IN_FLIGHT>();
+    issue_b_q8(st, kb + 1 < NKB ? kb + 1 : NKB - 1);
+    issue_a(st, kb + A_AHEAD < NKB ? kb + A_AHEAD : NKB - 1);
+  }
   const u4_t *as = &a_ring[kb % A_STAGES][0];
   const u4_t *bt = &bt_st[kb & 1][0][0];
   // LDS reads first: per row-block the four scales and this lane's 8 bytes of
@@ -421,7 +472,7 @@ __device__ __forceinline__ void mfma_step_q8(TileStateQ8<GATEUP, NTT> &st, int k
   for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
-      const int rb = (GATEUP ? m * RB_HALF : 0) + 16 * (RG * wave + rg) + lr;
+      const int rb = rb_pos<GATEUP>(wave, m, rg, lr);
       dsc[rg][m] = __builtin_bit_cast(f4_t, as[rb * RB_CHUNKS]);
       const u2_t *qp = reinterpret_cast<const u2_t *>(as + rb * RB_CHUNKS + 1);
 #pragma unroll
@@ -466,13 +517,8 @@ __device__ __forceinline__ void mfma_tile_q8(const uint8_t *__restrict__ wsh,
   S st;
   st.abase = wsh;
 #pragma unroll
-  for (int j = 0; j < A_DMA; j++) {
-    int c = A_CHUNKS_WAVE * wave + 64 * j + lane;
-    if (c >= A_CHUNKS) c = A_CHUNKS - 1;  // inactive lanes of the last copy
-    const int rb = c / RB_CHUNKS, pc = c % RB_CHUNKS;
-    const int m = GATEUP ? rb / RB_HALF : 2, lrow = GATEUP ? rb % RB_HALF : rb;
-    st.aoff[j] = (uint32_t)(m * Q8_MAT_BYTES + (rt * C::TROWS + lrow) * NKB * QB + 16 * pc);
-  }
+  for (int j = 0; j < A_DMA; j++)
+    st.aoff[j] = a_src<GATEUP>(wave, 64 * j + lane, rt, Q8_MAT_BYTES, NKB);
   st.a_last = 64 * (A_DMA - 1) + lane < A_CHUNKS_WAVE;
   // activations: copy j of wave w fills positions q = 64 (B8_DMA w + j) + lane
   // of the 32 x 16 chunk tile: row r = q / 16, position q % 16 holds chunk
