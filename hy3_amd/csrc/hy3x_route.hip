@@ -124,7 +124,12 @@ __device__ __forceinline__ void router_block(
   for (int q = tid; q < 8 * RS; q += 256) xsf[q] = (xsf[q] * wsf[q]) * r;  // s, in place
   __syncthreads();
   if (tid < 64) {  // the eight logit chains in wave 0
+    // the chain wave first at its SIMD's issue while the chains run: the shared
+    // expert's gate/up waves of the same launch compete for it (C0 29.9 ->
+    // 29.75 us; the whole router block at raised priority measured the same)
+    __builtin_amdgcn_s_setprio(3);
     const float lg = tree8_lanes(chain_lanes(rsf, xsf, tid), tid & 7);
+    __builtin_amdgcn_s_setprio(0);
     if (tid == 56) {
       const float sg = sigmoid_c(lg);
       logits[(size_t)t * E + e] = lg;
