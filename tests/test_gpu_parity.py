@@ -268,10 +268,11 @@ def test_rms_scale_override_is_switched_off(torch, layer, cpu):
 
 
 @pytest.mark.parametrize("K", [1, 2, 4])
-@pytest.mark.parametrize("T,path", [(1, 0), (40, 3), (40, 4), (40, 1)])
+@pytest.mark.parametrize("T,path", [(1, 0), (40, 3), (40, 4), (40, 1), (40, 5), (300, 5)])
 def test_output_top_k_variants(torch, layer, cpu, K, T, path):
-    """Top-K below 8 through every expert path (decode kernels, narrow and
-    wide MFMA tiles, GEMV tiles): routing bit-exact, output within TOL."""
+    """Top-K below 8 through every expert path (decode kernels, narrow, wide
+    and 128-token MFMA tiles, GEMV tiles): routing bit-exact, output within
+    TOL."""
     x = C.inputs(0xC6, T, first_token=7)
     rows = np.linspace(0, T - 1, min(T, 4)).astype(int)
     layer.set_path(path)
