@@ -18,14 +18,17 @@ __global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w
 // (register ring) per tile size: 4 x 8 (tiny), 8 x 16 (mid) and the larger
 // tiles. Few blocks run at small T, so each chunk's load latency must hide
 // behind the previous chunks' FMAs.
-constexpr int ROUTER_KC_TINY = 256, ROUTER_KC_MID = 256, ROUTER_KC_LARGE = 128;
-constexpr int ROUTER_R_TINY = 2, ROUTER_R_MID = 2, ROUTER_R_LARGE = 1;
+// The largest tile (32 x 32, T > 512) runs 64-wide chunks, four in flight
+// (router stage at 4096 tokens 205 -> 182 us; at 512 tokens, 16 x 16 tiles,
+// the same ring measured 54 -> 60 us, so that tile keeps 128-wide chunks).
+constexpr int ROUTER_KC_TINY = 256, ROUTER_KC_MID = 256, ROUTER_KC_LARGE = 128, ROUTER_KC_XL = 64;
+constexpr int ROUTER_R_TINY = 2, ROUTER_R_MID = 2, ROUTER_R_LARGE = 1, ROUTER_R_XL = 4;
 template <int MT, int ME, int TG, int EG, int KC, int R>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
                                                      float *logits);
 extern template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
     const float *, const float *, int, float *);
-extern template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
+extern template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_XL, ROUTER_R_XL>(
     const float *, const float *, int, float *);
 extern template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY>(
     const float *, const float *, int, float *);

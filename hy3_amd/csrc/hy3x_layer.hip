@@ -511,7 +511,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
           k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 15) / 16, E / 16), 256, 0, st>>>(
               S.s32, L->router, T, S.logits);
         else
-          k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
+          k_router_gemm<8, 4, 4, 8, ROUTER_KC_XL, ROUTER_R_XL><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
               S.s32, L->router, T, S.logits);
       }
       {

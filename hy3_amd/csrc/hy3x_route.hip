@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
       if (v == 0 && tt < T) logits[(size_t)tt * E + ee] = lg;
     }
 }
-template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
+template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_XL, ROUTER_R_XL>(
     const float *, const float *, int, float *);
 template __global__ void k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
     const float *, const float *, int, float *);
