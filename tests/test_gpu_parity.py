@@ -524,12 +524,13 @@ def test_mfma_tile_shapes_on_crowded_experts(torch, layer, cpu, T):
         cpu.bias = saved
 
 
-@pytest.mark.parametrize("T", [1, 64])
+@pytest.mark.parametrize("T", [1, 64, 400, 2100])
 def test_graph_replay_matches_eager(torch, layer, T):
     """The forward only enqueues kernels, so it can be captured in a HIP graph
     (as the engine captures its decode step). Every replay -- with eager work
     and other forwards on the same layer in between -- reproduces the eager
-    result bit for bit."""
+    result bit for bit, on the decode kernels and the narrow, wide and
+    128-token tiles."""
     x0 = torch.from_numpy(C.inputs(0xC2, T).copy()).cuda()
     xe = x0.clone()
     layer.forward(xe.data_ptr(), T, 8)
