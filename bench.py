@@ -157,15 +157,17 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
             residual=False, rotate=1):
     """Time `steps` forwards of cfg. A stacked config (n_layers > 1) runs all its
     layers per step. A one-layer config with rotate > 1 keeps `rotate` distinct
-    layers of the same distribution resident (layer indices 0 .. rotate-1, one
-    shared scratch) and step i runs layer i % rotate: with their weights far
+    layers of the same distribution resident (layer indices 0 .. rotate-1, each
+    with its own scratch) and step i runs layer i % rotate: with their weights far
     beyond the 256 MB last-level cache every step streams from HBM, as the
     layers of a real decode do (cold timing). rotate = 1 re-runs one layer
     (warm for a decode, whose 99 MB stay in the cache)."""
     n_inst = cfg.n_layers if cfg.n_layers > 1 else rotate
     layers = []
     for li in range(n_inst):
-        L = H.MoELayer(cfg.T, share_scratch_with=layers[0] if layers else None)
+        # each layer its own scratch: the stage replays below re-run a layer's
+        # kernels on the routing its own last forward left there
+        L = H.MoELayer(cfg.T)
         L.synth_experts(cfg.weight_seed, li)
         if shared_q8:
             L.synth_shared_q8_0(cfg.weight_seed, li)
@@ -306,6 +308,17 @@ def cpu_baseline(torch, H, C, cfg, seconds, shared_q8=False):
     L.close()
     ref = O.ref_lib()
     kind = "reference" if ref is not None else "port"
+    if ref is None:
+        # oracle/_ref is built from the reference sources in the development
+        # container and travels with the working tree; a clean checkout lacks it
+        print(f"bench.py: WARNING: {O.REF_LIB} is absent; cpu_baseline times the oracle port "
+              "(kind 'port'), not hy3.c's own forward_layer_moe", file=sys.stderr, flush=True)
+        ref_build = None
+    else:
+        import hashlib
+        with open(O.REF_LIB, "rb") as f:
+            ref_build = {"library": os.path.relpath(O.REF_LIB, ROOT),
+                         "sha256": hashlib.sha256(f.read()).hexdigest()}
     cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     if ref is not None:
@@ -324,7 +337,7 @@ def cpu_baseline(torch, H, C, cfg, seconds, shared_q8=False):
         if el >= seconds or n >= 100000:
             break
     return dict(value=round(n / el, 3), unit="tokens/s", cores=cores, kind=kind,
-                cpu_model=cpu_model(),
+                reference_build=ref_build, cpu_model=cpu_model(),
                 prefill_note="hy3.c runs a prefill's MoE one token at a time (hy3_gpu.cu:836-837, "
                              "hy3.c per-token forward), so its prefill tokens/s equals this rate",
                 sample=f"{n} tokens of config {cfg.index}, one at a time as hy3.c runs its MoE "

@@ -50,6 +50,7 @@ struct ScratchMem {
   uint8_t *mem = nullptr;
   int max_tokens = 0;
   int refs = 1;
+  const hy3x_layer *owner = nullptr;  // the layer whose forward ran on it last
 };
 static std::mutex g_scratch_mu;
 
@@ -78,6 +79,7 @@ struct hy3x_layer {
     bool big = false;   // MFMA mode: 128-token tiles (mfma_big)
     const float *r_in = nullptr;  // substituted RMSNorm scales, or null
     Scratch sc;         // the scratch this forward runs on
+    const hy3x_layer **owner = nullptr;  // that scratch's last-forward owner slot
   } cur;
   hipStream_t last_stream = nullptr;
   int path = 0;
@@ -266,6 +268,7 @@ static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 constexpr int kMaxDevices = 64;
 static std::mutex g_static_mu;
 static uint8_t *g_static_ptr[kMaxDevices];
+static const hy3x_layer *g_static_owner[kMaxDevices];  // last layer to run on `scratch`
 
 // This device's address of `scratch` (looked up on the device's first call).
 static int static_scratch_ptr(int device, uint8_t **out) {
@@ -586,11 +589,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
   }
 }
 
-static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float *xadd, int T,
-                        int K, float scale, void *stream);
+static int forward_impl(hy3x_layer *L, const Scratch *sc, const hy3x_layer **owner, float *x,
+                        const float *xadd, int T, int K, float scale, void *stream);
 
 int hy3x_layer_forward(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
-  return forward_impl(L, L ? &L->own : nullptr, x, nullptr, T, K, scale, stream);
+  return forward_impl(L, L ? &L->own : nullptr, L ? &L->scratch_mem->owner : nullptr, x,
+                      nullptr, T, K, scale, stream);
 }
 
 int hy3x_layer_forward_static(hy3x_layer *L, float *x, int T, int K, float scale, void *stream) {
@@ -607,7 +611,7 @@ int hy3x_layer_forward_static(hy3x_layer *L, float *x, int T, int K, float scale
   const int rc = static_scratch_ptr(dev, &base);
   if (rc) return rc;
   const Scratch sc = scratch_layout(HY3X_STATIC_MAX_TOKENS, base);
-  return forward_impl(L, &sc, x, nullptr, T, K, scale, stream);
+  return forward_impl(L, &sc, &g_static_owner[dev], x, nullptr, T, K, scale, stream);
 }
 
 int hy3x_layer_forward_residual(hy3x_layer *L, float *x, const float *attn_out, int T, int K,
@@ -619,12 +623,13 @@ int hy3x_layer_forward_residual(hy3x_layer *L, float *x, const float *attn_out, 
     const uintptr_t n = (uintptr_t)T * D * sizeof(float);
     if (a0 < b0 + n && b0 < a0 + n) return fail(HY3X_E_ARG, "attn_out overlaps x");
   }
-  return forward_impl(L, L ? &L->own : nullptr, x, attn_out, T, K, scale, stream);
+  return forward_impl(L, L ? &L->own : nullptr, L ? &L->scratch_mem->owner : nullptr, x,
+                      attn_out, T, K, scale, stream);
 }
 
-static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float *xadd, int T,
-                        int K, float scale, void *stream) {
-  if (!L || !x || !sc) return fail(HY3X_E_ARG, "NULL argument");
+static int forward_impl(hy3x_layer *L, const Scratch *sc, const hy3x_layer **owner, float *x,
+                        const float *xadd, int T, int K, float scale, void *stream) {
+  if (!L || !x || !sc || !owner) return fail(HY3X_E_ARG, "NULL argument");
   if (T < 1 || T > sc->max_tokens)
     return fail(HY3X_E_ARG, "T=%d outside [1,%d]", T, sc->max_tokens);
   if (K < 1 || K > KMAX) return fail(HY3X_E_ARG, "K=%d outside [1,8]", K);
@@ -638,6 +643,7 @@ static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float 
   c.scale = scale;
   c.sc = *sc;
   c.r_in = L->rms_n >= T ? L->rms_r : nullptr;
+  L->rms_n = 0;  // a substituted scale serves one forward only
   if (T == 1 && L->path == 0)
     c.mode = Mode::DECODE;
   else if (L->path >= 2 || (L->path == 0 && T >= kMfmaMinT))
@@ -668,6 +674,8 @@ static int forward_impl(hy3x_layer *L, const Scratch *sc, float *x, const float 
   L->last_T = T;
   L->last_K = K;
   L->last_stream = st;
+  c.owner = owner;
+  *owner = L;
   return HY3X_OK;
 }
 
@@ -756,6 +764,9 @@ int hy3x_layer_last_routing(hy3x_layer *L, int32_t *ids, float *wpre, float *w,
   if (capacity < n)
     return fail(HY3X_E_ARG, "routing buffers hold %lld entries, the last forward has %d x %d",
                 (long long)capacity, L->last_T, L->last_K);
+  if (!L->cur.owner || *L->cur.owner != L)
+    return fail(HY3X_E_STATE,
+                "the scratch of this layer's last forward has since run another layer's forward");
   HIP_TRY(hipStreamSynchronize(L->last_stream));
   const Scratch &S = L->cur.sc;
   if (ids) HIP_TRY(hipMemcpy(ids, S.ids, n * sizeof(int32_t), hipMemcpyDeviceToHost));

@@ -112,6 +112,13 @@ int hy3_gpu_init(hy3_model *m, int n_gpu_layers) {
   if (!m) return -1;
   if (m->gpu_ctx) hy3_gpu_free(m);
   if (n_gpu_layers <= 0 || n_gpu_layers > MOE_MAX_GPU_LAYERS) n_gpu_layers = MOE_MAX_GPU_LAYERS;
+  if (n_gpu_layers <= HY3_N_LAYER_DENSE) {
+    /* [HY3_N_LAYER_DENSE, n_gpu_layers) holds no MoE layer: nothing would run
+     * on the GPU, so report failure and let the caller stay on the CPU */
+    fprintf(stderr, "hy3_gpu: n_gpu_layers %d covers no MoE layer (the first is layer %d)\n",
+            n_gpu_layers, HY3_N_LAYER_DENSE);
+    return -1;
+  }
   for (int il = HY3_N_LAYER_DENSE; il < n_gpu_layers; il++)
     if (check_layer(&m->w.layers[il], il)) return -1;
   moe_ctx *c = (moe_ctx *)calloc(1, sizeof(moe_ctx));

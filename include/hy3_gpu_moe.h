@@ -4,8 +4,19 @@
  *
  * This header and hy3_amd/engine/hy3_gpu_moe.c are compiled by the engine,
  * against its own hy3.h (the hy3_model / hy3_layer_weights / hy3_weight
- * types, hy3.h:107-217), into libhy3gpu_moe.so. hy3.o and hy3_cli.o link
- * against the first two symbols unchanged.
+ * types, hy3.h:107-217), into libhy3gpu_moe.so. The engine's sources need
+ * edits to use it; they do NOT link unchanged:
+ *  - hy3.c built with -DHY3_CUDA calls hy3_eval_gpu (hy3.c:1368-1371), the
+ *    whole-token GPU engine (attention, KV cache, LM head), which this library
+ *    does not export, and would hand it a gpu_ctx of another type. Build the
+ *    engine WITHOUT HY3_CUDA;
+ *  - without HY3_CUDA, hy3_cli.c (:278-285) and hy3_agent.c (:591-592) never
+ *    call hy3_gpu_init and hy3_model_free (hy3.c:926-929) never calls
+ *    hy3_gpu_free: the application calls hy3_gpu_init after hy3_model_load
+ *    and hy3_gpu_free before hy3_model_free itself;
+ *  - forward_layer_moe (hy3.c:1264-1266) gets one line that hands its MoE half
+ *    to hy3_gpu_ffn_moe_host when m->gpu_ctx is set.
+ * The exact edits are listed where this library's integration is documented.
  *
  * Reference interface replaced (yuhai-china/hy3):
  *  - hy3_gpu_init   hy3_gpu.cu:544 (prototype hy3_gpu.h:6, hy3.c:1359,
@@ -40,7 +51,9 @@
 extern "C" {
 #endif
 
-/* hy3_gpu.cu:544. 0 on success; -1 on any error, with m->gpu_ctx NULL. */
+/* hy3_gpu.cu:544. 0 on success; -1 on any error, with m->gpu_ctx NULL. An
+ * n_gpu_layers of 1 .. HY3_N_LAYER_DENSE (no MoE layer in range) is an error:
+ * the caller keeps the CPU path. */
 int hy3_gpu_init(hy3_model *m, int n_gpu_layers);
 
 /* hy3_gpu.cu:632. Frees everything hy3_gpu_init made; m->gpu_ctx = NULL. */

@@ -150,8 +150,8 @@ int hy3x_layer_forward(hy3x_layer *layer, float *x, int T, int K, float scale, v
  * hy3x_layer_forward, same result bit for bit. Call it with the layer's
  * device current. Every call on one GPU shares that GPU's array, whatever the
  * layer: calls that overlap on one GPU (other streams, other threads) race,
- * and hy3x_layer_last_routing reads the array as the last static call left
- * it. Calls no hipMalloc, hipFree or allocating library routine. */
+ * and hy3x_layer_last_routing of a layer refuses (HY3X_E_STATE) once another
+ * layer's static call has run. Calls no hipMalloc, hipFree or allocating library routine. */
 int hy3x_layer_forward_static(hy3x_layer *layer, float *x, int T, int K, float scale,
                               void *stream);
 
@@ -174,7 +174,10 @@ int hy3x_layer_last_shape(const hy3x_layer *layer, int *T, int *K);
  * stream): ids[T x K] int32 in selection order, wpre[T x K] = sigma / sum
  * (before the scale), w[T x K] (after). Any pointer may be NULL. capacity:
  * the number of entries each non-NULL buffer holds; HY3X_E_ARG if it is
- * below T x K of the last forward (nothing is copied then). */
+ * below T x K of the last forward (nothing is copied then). HY3X_E_STATE when
+ * the scratch that forward ran on has since run another layer's forward
+ * (layers made with hy3x_layer_create_shared, or hy3x_layer_forward_static
+ * calls of other layers): the routing it held is gone. */
 int hy3x_layer_last_routing(hy3x_layer *layer, int32_t *ids, float *wpre, float *w,
                             int64_t capacity);
 
@@ -228,10 +231,13 @@ int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_to
  * REALTIME-counter (100 MHz) checkpoints. */
 int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
 
-/* Diagnostics: substitute the RMSNorm scale. From this call on, a forward of
- * T <= n tokens uses r[t] (host array of n floats, copied) as token t's
- * 1/sqrt(mean(x^2) + 1e-5) instead of computing it; s = (x * norm_w) * r[t]
- * as before. n = 0 switches back to the computed scale. No reference
+/* Diagnostics: substitute the RMSNorm scale for ONE forward. The next forward
+ * of this layer, if it has T <= n tokens, uses r[t] (host array of n floats,
+ * copied) as token t's 1/sqrt(mean(x^2) + 1e-5) instead of computing it;
+ * s = (x * norm_w) * r[t] as before. That forward consumes the override
+ * (whatever its T): every later forward computes the scale again, so a
+ * forgotten override cannot leak into production routing. n = 0 cancels a
+ * pending override. No reference
  * counterpart: it lets a test feed the reference CPU build's own r (from the
  * host's rsqrt estimate and a Newton step, hy3.c:435-444 as compiled) and
  * compare the rest of the routing to it. */

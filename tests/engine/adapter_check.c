@@ -148,6 +148,10 @@ static int validate(void) {
   CHECK(hy3_gpu_init(m, 3) == -1 && m->gpu_ctx == NULL,
         "layer 2 without MoE tensors refused (n_gpu_layers 3)");
 
+  bind_layer(m, 1, li, small, small, small, ex, 12);
+  CHECK(hy3_gpu_init(m, 1) == -1 && m->gpu_ctx == NULL,
+        "n_gpu_layers 1 covers only the dense layer: refused");
+
   float x[D];
   CHECK(hy3_gpu_ffn_moe(m, 1, x, 1, NULL) == -1, "forward without a context fails");
   CHECK(hy3_gpu_ffn_moe_host(m, 1, x, 1) == -1, "host forward without a context fails");

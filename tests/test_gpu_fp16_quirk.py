@@ -69,24 +69,54 @@ def torch():
     return t
 
 
-@pytest.fixture(scope="module")
-def quirk_layer(torch):
-    """A layer whose experts used by the test tokens carry quirk blocks, and its
+def make_quirk_layer(T, seed):
+    """A layer whose experts used by T test tokens carry quirk blocks, and its
     oracle twin holding the same bytes."""
-    L = H.MoELayer(8)
+    L = H.MoELayer(T)
     L.synth_experts(C.WEIGHT_SEED, 0)
     nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
     L.set_router(nw, rt, b)
     cpu = O.SynthLayer(C.WEIGHT_SEED)
-    x = C.inputs(0xC8, 8)
+    x = C.inputs(seed, T)
     used = set(cpu.route(x)["ids"].ravel().tolist()) | {E}
     for e in sorted(used):
         mats = [patch(hipmem.to_host(L.expert_ptr(e, m), H.Q4K_MATRIX_BYTES), e + m)
                 for m in range(3)]
         L.set_expert_q4k(e, *mats)
         cpu.experts[e] = tuple(mats)
+    return L, cpu, x
+
+
+@pytest.fixture(scope="module")
+def quirk_layer(torch):
+    L, cpu, x = make_quirk_layer(8, 0xC8)
     yield L, cpu, x
     L.close()
+
+
+@pytest.fixture(scope="module")
+def quirk_layer_130(torch):
+    """130 tokens: the 128-token tiles run a full token tile and a ragged one."""
+    L, cpu, x = make_quirk_layer(130, 0xCA)
+    yield L, cpu, x
+    L.close()
+
+
+def run_path(torch, L, cpu, xs, path):
+    T = xs.shape[0]
+    xd = torch.from_numpy(xs.copy()).cuda()
+    L.set_path(path)
+    try:
+        L.forward(xd.data_ptr(), T)
+        torch.cuda.synchronize()
+        ids, wpre, _ = L.last_routing(T, 8)
+    finally:
+        L.set_path(0)
+    y = xd.cpu().numpy()
+    yo, ro = cpu.forward(xs)
+    assert np.array_equal(ids, ro["ids"])
+    assert np.array_equal(wpre.view(np.uint32), ro["wpre"].view(np.uint32))
+    assert O.rel_l2(y - xs, yo - xs) <= TOL
 
 
 def test_contrast_decoder_matches_oracle_on_normal_blocks():
@@ -103,25 +133,39 @@ def test_quirk_blocks_differ_from_ieee():
     assert (a[0::2] != b[0::2]).any(axis=1).all()  # every patched block decodes differently
 
 
-@pytest.mark.parametrize("T,path", [(1, 0), (8, 1), (8, 3), (8, 4), (1, 2)])
+@pytest.mark.parametrize("T,path", [(1, 0), (8, 1), (8, 3), (8, 4), (8, 5), (1, 2)])
 def test_quirk_blocks_on_every_path(torch, quirk_layer, T, path):
-    """Decode kernels (T = 1), GEMV tiles, narrow and wide MFMA tiles, and MFMA
-    at T = 1: routing bit-exact, output within TOL of the oracle."""
+    """Decode kernels (T = 1), GEMV tiles, narrow, wide and 128-token MFMA
+    tiles, and MFMA at T = 1: routing bit-exact, output within TOL of the
+    oracle."""
     L, cpu, x = quirk_layer
-    xs = x[:T]
-    xd = torch.from_numpy(xs.copy()).cuda()
-    L.set_path(path)
+    run_path(torch, L, cpu, x[:T], path)
+
+
+@pytest.mark.parametrize("path", [4, 5])
+def test_quirk_blocks_130_tokens(torch, quirk_layer_130, path):
+    """130 tokens through the wide and the 128-token tiles (a full and a ragged
+    token tile per hot expert)."""
+    L, cpu, x = quirk_layer_130
+    run_path(torch, L, cpu, x, path)
+
+
+@pytest.mark.parametrize("T,path", [(1, 0), (8, 3), (8, 4), (8, 5)])
+def test_quirk_blocks_with_q8_shared(torch, quirk_layer, T, path):
+    """The routed experts' quirk blocks on the kernels' Q8_0-shared variants
+    (hy3's real-checkpoint shared expert: the decode kernels and the narrow,
+    wide and 128-token MFMA tiles with mfma_tile_q8): routing bit-exact, output
+    within TOL of the oracle holding the same Q8_0 shared expert."""
+    L, cpu, x = quirk_layer
+    q8 = tuple(O.gen_matrix_q8(C.WEIGHT_SEED, 0, k, E) for k in (O.T_GATE, O.T_UP, O.T_DOWN))
+    o = O.SynthLayer(C.WEIGHT_SEED, shared_q8=True)
+    o.experts = {e: m for e, m in cpu.experts.items() if e != E}
+    o.experts[E] = q8
+    L.set_shared_q8_0(*q8)
     try:
-        L.forward(xd.data_ptr(), T)
-        torch.cuda.synchronize()
-        ids, wpre, _ = L.last_routing(T, 8)
+        run_path(torch, L, o, x[:T], path)
     finally:
-        L.set_path(0)
-    y = xd.cpu().numpy()
-    yo, ro = cpu.forward(xs)
-    assert np.array_equal(ids, ro["ids"])
-    assert np.array_equal(wpre.view(np.uint32), ro["wpre"].view(np.uint32))
-    assert O.rel_l2(y - xs, yo - xs) <= TOL
+        L.set_expert_q4k(E, *cpu.experts[E])
 
 
 def test_ieee_decode_would_fail(quirk_layer):

@@ -267,6 +267,46 @@ def test_rms_scale_override_is_switched_off(torch, layer, cpu):
     assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
 
 
+def test_last_routing_refused_after_another_layers_forward(torch):
+    """Layers sharing one scratch: once layer B has run, layer A's routing is
+    gone from the scratch and hy3x_layer_last_routing(A) says so instead of
+    returning B's ids."""
+    nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
+    A = H.MoELayer(4)
+    Bl = H.MoELayer(4, share_scratch_with=A)
+    try:
+        for L in (A, Bl):
+            L.synth_experts(C.WEIGHT_SEED, 0)
+            L.set_router(nw, rt, b)
+        x = torch.from_numpy(C.inputs(0xC0, 2).copy()).cuda()
+        A.forward(x.data_ptr(), 2)
+        torch.cuda.synchronize()
+        A.last_routing(2, 8)
+        Bl.forward(x.data_ptr(), 2)
+        torch.cuda.synchronize()
+        Bl.last_routing(2, 8)
+        with pytest.raises(H.HY3XError, match="another layer"):
+            A.last_routing(2, 8)
+    finally:
+        Bl.close()
+        A.close()
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_rms_scale_override_serves_one_forward(torch, layer, cpu, T):
+    """An override left set is consumed by the next forward: the forward after
+    it, with no clearing call, routes with the computed scale again (equal to
+    the oracle bit for bit), while the overridden forward itself did not."""
+    x = C.inputs(0xC1, T)
+    r = cpu.route(x)
+    layer.set_rms_scale(np.full(T, 0.37, np.float32))
+    _, ids0, wpre0, _ = run(torch, layer, x)
+    assert not np.array_equal(wpre0.view(np.uint32), r["wpre"].view(np.uint32))
+    _, ids, wpre, _ = run(torch, layer, x)
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
+
+
 @pytest.mark.parametrize("K", [1, 2, 4])
 @pytest.mark.parametrize("T,path", [(1, 0), (40, 3), (40, 4), (40, 1), (40, 5), (300, 5)])
 def test_output_top_k_variants(torch, layer, cpu, K, T, path):
