@@ -118,18 +118,18 @@ def default_steps(T, n_layers):
 
 def stage_bytes(stage, U, T, K, decode, shared_q8=False):
     """Algorithmic HBM bytes of one launch of a kernel stage. Single-token
-    decode: the gate/up stage is one launch holding the router (router matrix,
-    norm weight, bias, x), the shared expert's gate/up and the K routed
-    experts' gate/up, writing h; the router stage launches nothing.
-    shared_q8: the shared expert's matrices are hy3 Q8_0 (Q8MAT bytes each)."""
+    decode: the router stage also streams the shared expert's gate/up and the
+    gate/up stage streams the K routed experts only. shared_q8: the shared
+    expert's matrices are hy3 Q8_0 (Q8MAT bytes each)."""
     sh = Q8MAT if shared_q8 else MAT
     router = 192 * 4096 * 4 + 4096 * 4 + T * 4096 * 4 + T * 4096 * 6
     if decode:
         if stage == "gateup":
-            return (192 * 4096 * 4 + 4096 * 4 + 192 * 4 + 4096 * 4 + 2 * sh
-                    + K * 2 * MAT + (K + 1) * 1536 * 2)
+            return K * 2 * MAT + 4096 * 2 + K * 1536 * 2
         if stage == "down":
             return K * MAT + sh + (K + 1) * 1536 * 2 + 2 * 4096 * 4
+        if stage == "router":
+            return router + 2 * sh + 1536 * 2
         return 0
     if stage == "gateup":
         return (U - 1) * 2 * MAT + 2 * sh + T * 4096 * 2 + T * (K + 1) * 1536 * 2
@@ -144,7 +144,7 @@ def dominant_kernel(stage, last_path):
     """Kernel name of a stage on the path the last forward ran
     (hy3x_layer_last_path)."""
     if last_path == 0:
-        return {"gateup": "k_decode_gateup", "down": "k_down_decode"}[stage]
+        return {"gateup": "k_gateup_decode", "down": "k_down_decode"}[stage]
     if last_path == 5:
         return {"gateup": "mfma_big::k_moe_big<true>", "down": "mfma_big::k_moe_big<false>"}[stage]
     if last_path in (3, 4):
@@ -217,14 +217,12 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
     torch.cuda.synchronize()
     for L in layers:
         L.stats(reset=True)
-        L.decode_stats(reset=True)
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     fw, touched = zip(*[L.stats(reset=True) for L in layers])
-    unc, expired = (sum(v) for v in zip(*[L.decode_stats(reset=True) for L in layers]))
     U = sum(touched) / max(sum(fw), 1)  # mean experts touched per layer-forward
     ms = elapsed * 1e3 / steps
     tokens_per_s = cfg.T * steps / elapsed
@@ -264,8 +262,7 @@ def measure(torch, H, C, cfg, steps, warmup, use_graph=False, path=0, shared_q8=
     for L in layers:
         L.close()
     return dict(
-        tokens_per_s=tokens_per_s, ms_per_step=ms, U=U, uncertified=unc, expired_waits=expired,
-        forwards=sum(fw), layer_GBps=alg_bytes / (ms * 1e-3) / 1e9,
+        tokens_per_s=tokens_per_s, ms_per_step=ms, U=U, layer_GBps=alg_bytes / (ms * 1e-3) / 1e9,
         layer_TFLOPs=flops / (ms * 1e-3) / 1e12, stage_us=stage_us,
         roofline=(dict(bound="mfma", kernel=kernel, achieved=round(tflops, 1),
                        peak=PEAK_MFMA_TFLOPS, unit="TFLOP/s",
@@ -399,10 +396,6 @@ def main():
                    "shared_expert": "q8_0" if a.shared_q8 else "q4_k",
                    "entry": "forward_residual" if a.residual else "forward"},
         "layer": {"experts_touched": round(r["U"], 2), "GB_per_s": round(r["layer_GBps"], 1),
-                  **({"decode_routing": {"forwards": r["forwards"],
-                                         "certified_early": r["forwards"] - r["uncertified"],
-                                         "expired_waits": r["expired_waits"]}}
-                     if cfg.T == 1 else {}),
                   "hbm_frac": round(r["layer_GBps"] / PEAK_HBM_GBS, 4),
                   "stage_us": {k: round(v, 2) for k, v in r["stage_us"].items()}},
         "roofline": r["roofline"],

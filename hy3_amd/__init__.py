@@ -73,7 +73,6 @@ _SIGS = {
     "hy3x_layer_set_timing": (I32, [P, I32]),
     "hy3x_layer_set_trace": (I32, [P, I32, P]),
     "hy3x_layer_stats": (I32, [P, ctypes.POINTER(U64), ctypes.POINTER(U64), I32]),
-    "hy3x_layer_decode_stats": (I32, [P, ctypes.POINTER(U64), ctypes.POINTER(U64), I32]),
     "hy3x_layer_stage_times": (I32, [P, P, I32, ctypes.POINTER(I32)]),
     "hy3x_synth_layer_experts": (I32, [P, U64, U32]),
     "hy3x_synth_quantize_q4k": (I32, [P, P, I64, P]),
@@ -277,13 +276,6 @@ class MoELayer:
         f, u = U64(), U64()
         _check(lib().hy3x_layer_stats(self._h, ctypes.byref(f), ctypes.byref(u), 1 if reset else 0))
         return f.value, u.value
-
-    def decode_stats(self, reset=True):
-        """(decode forwards whose routing was not certified early, expired waits)."""
-        a, b = U64(), U64()
-        _check(lib().hy3x_layer_decode_stats(self._h, ctypes.byref(a), ctypes.byref(b),
-                                             1 if reset else 0))
-        return a.value, b.value
 
     def forward(self, x_dev_ptr, T, K=K_MAX, scale=ROUTE_SCALE, stream=None):
         """In-place MoE block on device memory x[T x 4096] (fp32)."""

@@ -127,37 +127,15 @@ constexpr int DEC_GU_PF = 2;                 // gate/up rows in flight per wave 
 constexpr int DEC_SH_RPW = 1;
 constexpr int DEC_RPB = 4 * DEC_SH_RPW;       // shared gate/up rows per routing block (four waves)
 static_assert(F % DEC_RPB == 0, "the routing kernel's shared blocks cover every row");
-constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the first launch (384)
+constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (384)
 // Waves per routed gate/up block (each block routes the token once, then its
 // waves stream DEC_RPW rows each).
 constexpr int DEC_GU_WAVES = 4;
 constexpr int DEC_GU_RPB = DEC_GU_WAVES * DEC_RPW;  // routed gate/up rows per block
 static_assert(F % DEC_GU_RPB == 0, "whole blocks per expert");
 constexpr int DEC_GU_BLOCKS = F / DEC_GU_RPB;       // routed gate/up blocks per expert
-// Blocks of the first decode launch (k_decode_gateup): KMAX slots of routed
-// gate/up blocks; blocks 0 .. E - 1 are also the router blocks, E .. E +
-// DEC_SH_BLOCKS - 1 also carry the shared expert's gate/up rows.
-constexpr int DEC_BLOCKS = KMAX * DEC_GU_BLOCKS;
-static_assert(E + DEC_SH_BLOCKS <= DEC_BLOCKS, "router and shared roles fit the launch");
-
-// Cross-block words of the first decode launch, in the forward scratch
-// (tagged words: value bits | forward tag << 32).
-struct DecodeSync {
-  uint32_t *epoch;     // [1] tag of the last completed launch
-  uint32_t *started;   // [DEC_BLOCKS] tag of each block's launch, written at its start
-  uint64_t *bound_lo;  // [E] lower bound of each expert's biased score
-  uint64_t *bound_hi;  // [E] upper bound (= bound_lo + E)
-  uint64_t *sig;       // [E] exact sigmoid of each logit
-  uint64_t *spec;      // [KMAX] the expert of each routed gate/up slot (bits of an int)
-  int32_t *spec_ids;   // [KMAX] the same, plain, for the down launch
-  int32_t *perm;       // [KMAX] for the exact top-K's place kk, the slot holding its expert
-};
-constexpr size_t DEC_SYNC_BYTES = 256 + DEC_BLOCKS * 4 + 3 * E * 8 + KMAX * 8 + 2 * KMAX * 4;
 constexpr int DEC_DOWN_RPB = 16;  // down rows per block
-#ifndef HY3X_DOWN_PF
-#define HY3X_DOWN_PF 2
-#endif
-constexpr int DEC_DOWN_PF = HY3X_DOWN_PF;  // down passes (2 rows each) in flight per wave
+constexpr int DEC_DOWN_PF = 2;    // down passes (2 rows each) in flight per wave
 // Waves of a down block: one per routed slot, then the shared expert's rows
 // split over DEC_DOWN_SH_WAVES waves, so that every SIMD runs the same number
 // of passes (with one shared wave, the SIMD holding three waves set the pace).

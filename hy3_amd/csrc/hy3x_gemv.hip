@@ -155,13 +155,91 @@ __global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ w
 // Decode fast path (T = 1): no dispatch. Slot k < K is routed expert ids[k],
 // slot K the shared expert; the expert id is one load away from the weights.
 
+// Routed gate/up of a single token: block = DEC_GU_RPB rows (DEC_GU_WAVES
+// waves x 4) of routed slot blockIdx.x / DEC_GU_BLOCKS. Every wave routes the
+// token itself from the 192 sigmoid values / scores (the routing contract,
+// identical in every wave and block: topk_wave_fast, or topk_wave_regs on a
+// tie) and takes the expert of its slot; block 0 publishes the routing and
+// the stats. All blocks are resident at once.
+__global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
+    const uint8_t *__restrict__ wq, const __half *__restrict__ s16,
+    const float *__restrict__ sig, const float *__restrict__ score, int K, float scale,
+    int32_t *__restrict__ ids, float *__restrict__ wpre, float *__restrict__ wout,
+    unsigned long long *__restrict__ stats, __half *__restrict__ h16,
+    unsigned long long *trace) {
+  trace_point(trace, 0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = blockIdx.x / DEC_GU_BLOCKS, rc = blockIdx.x % DEC_GU_BLOCKS;
+  // the token's staged s, once per block (the four waves read it from LDS),
+  // loaded together with the routing inputs
+  const int tid = threadIdx.x;
+  constexpr int NT = 64 * DEC_GU_WAVES, NS = (D / 8 + NT - 1) / NT;  // 16-byte pieces per thread
+  constexpr bool EXACT = NS * NT == D / 8;
+  uint4 sv[NS];
+#pragma unroll
+  for (int i = 0; i < NS; i++)
+    sv[i] = EXACT || tid + NT * i < D / 8 ? reinterpret_cast<const uint4 *>(s16)[tid + NT * i]
+                                          : make_uint4(0u, 0u, 0u, 0u);
+  // the routing inputs: expert lane + 64 m's score and sigma
+  float sc[3], sg[3];
+#pragma unroll
+  for (int m = 0; m < 3; m++) {
+    sc[m] = score[lane + 64 * m];
+    sg[m] = sig[lane + 64 * m];
+  }
+  __shared__ __attribute__((aligned(16))) __half s_l[D];
+  __shared__ int32_t sids[KMAX];
+  __shared__ float swp[KMAX], sw[KMAX];
+#pragma unroll
+  for (int i = 0; i < NS; i++)
+    if (EXACT || tid + NT * i < D / 8) reinterpret_cast<uint4 *>(s_l)[tid + NT * i] = sv[i];
+  // every wave routes the token itself, in registers (the same arithmetic in
+  // every wave and block, so the outcome is block-uniform)
+  int my_e;
+  float my_sig, sum;
+  // a block needs the first slot + 1 places only (block 0, which publishes
+  // the routing, all K): places before a tie are the same in every method.
+  // (Issuing the first weight loads before the activation reads below, as
+  // the shared-expert blocks do, measured 4 us slower here.)
+  const bool fast = topk_wave_fast(sc, sg, blockIdx.x == 0 ? K : slot + 1, my_e, my_sig, sum);
+  __syncthreads();  // s_l staged
+  int e;
+  if (fast) {
+    e = __builtin_amdgcn_readlane(my_e, slot);
+    if (blockIdx.x == 0 && threadIdx.x < K) {
+      const float inv = 1.0f / (sum + 1e-20f);
+      const float v = my_sig * inv;
+      ids[threadIdx.x] = my_e;
+      wpre[threadIdx.x] = v;
+      wout[threadIdx.x] = v * scale;
+    }
+  } else {  // a tie or a NaN among the scores: the reference's selection with swaps
+    if (wave == 0) topk_wave_regs(sc, sg, K, scale, sids, swp, sw);
+    __syncthreads();
+    e = sids[slot];
+    if (blockIdx.x == 0 && threadIdx.x < K) {
+      ids[threadIdx.x] = sids[threadIdx.x];
+      wpre[threadIdx.x] = swp[threadIdx.x];
+      wout[threadIdx.x] = sw[threadIdx.x];
+    }
+  }
+  uint32_t X[32];
+  load_group_x(s_l, lane, X);
+  float slo, shi;
+  group_sums(X, slo, shi);
+  trace_point(trace, 1);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && stats) {  // forwards, experts touched (shared included)
+    stats[0] += 1ull;
+    stats[1] += (unsigned long long)(K + 1);
+  }
+  gateup_rows<DEC_RPW, DEC_GU_PF>(wq, e, slot, rc * DEC_GU_RPB + wave * DEC_RPW, X, slo, shi,
+                                  h16);
+  trace_point(trace, 3);
+}
+
 // Down of a single token for rows blockIdx.x*RPB .. +RPB, fused with the
 // combine y = x + (shared + sum_k w_k * down_k), k in selection order
-// (hy3.c:1302, 1318-1319, 1324-1325). Slot j < K holds the h of expert
-// spec[j] (the slot order the gate/up launch streamed in: the exact top-K's
-// set, in another order when its routing was certified early; perm[kk] is
-// the slot of the exact kk-th place), and the combine takes the slots in the
-// exact order with their exact weights w. Wave k < K owns slot k, waves
+// (hy3.c:1302, 1318-1319, 1324-1325). Wave k < K owns routed slot k, waves
 // KMAX .. KMAX + 3 a quarter of the rows each of the shared expert (waves
 // K .. KMAX - 1 are idle): their passes of 2 rows stream through a register
 // ring of DEC_DOWN_PF passes (down_rows; 2 measured best), the row sums go
@@ -173,27 +251,23 @@ __global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ w
 // 157 KB of LDS per block keeps a block off a CU until the CU is empty.
 __global__ __launch_bounds__(64 * DEC_DOWN_WAVES) void k_down_decode(
     const uint8_t *__restrict__ wq, const __half *__restrict__ h16,
-    const int32_t *__restrict__ spec, const int32_t *__restrict__ perm,
-    const float *__restrict__ w, int K, float *__restrict__ x, const float *__restrict__ xadd,
-    const uint8_t *__restrict__ wsh, unsigned long long *trace) {
+    const int32_t *__restrict__ ids, const float *__restrict__ w, int K,
+    float *__restrict__ x, const float *__restrict__ xadd, const uint8_t *__restrict__ wsh,
+    unsigned long long *trace) {
   constexpr int RPB = DEC_DOWN_RPB, SH_ROWS = RPB / DEC_DOWN_SH_WAVES;
   __shared__ float out_l[KMAX + 1][RPB];  // [KMAX]: the shared expert
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int r0 = blockIdx.x * RPB;
-  // the combine's inputs (residual row; for each exact place kk in lane kk,
-  // its weight and the slot holding its expert), loaded before the weight
-  // streams so that they are in registers when the row sums are (raw values:
-  // an add here would wait for the loads)
+  // the combine's inputs (residual row, gate weights), loaded before the
+  // weight streams so that they are in registers when the row sums are
+  // (raw values: an add here would wait for the loads)
   float xv = 0.0f, xav = 0.0f, wv = 0.0f;
-  int pj = 0;
   if (k == 0) {
     const int r = r0 + (lane < RPB ? lane : 0);
     xv = x[r];
     if (xadd) xav = xadd[r];
-    const int kl = lane < K ? lane : 0;
-    wv = w[kl];
-    pj = perm[kl];
+    wv = w[lane < K ? lane : 0];  // lane kk holds w[kk]
   }
   if (k >= KMAX) {  // a quarter of the block's rows of the shared expert
     const int q = k - KMAX;
@@ -216,24 +290,17 @@ __global__ __launch_bounds__(64 * DEC_DOWN_WAVES) void k_down_decode(
       }
     };
     const int ku = __builtin_amdgcn_readfirstlane(k);  // a scalar load of the id
-    down_rows<RPB / 2, DEC_DOWN_PF>(
-        wq, [&] { const int e = spec[ku]; return e >= 0 && e < E ? e : 0; },
-        h16 + (size_t)k * F, r0, keep);
+    down_rows<RPB / 2, DEC_DOWN_PF>(wq, [&] { return ids[ku]; }, h16 + (size_t)k * F, r0, keep);
   }
   __syncthreads();
   trace_point(trace, 2);
   if (threadIdx.x < RPB) {
     const int r = r0 + threadIdx.x;
     float eo = 0.0f;
-    for (int kk = 0; kk < K; kk++) {
-      const int j = __builtin_amdgcn_readlane(pj, kk);
-      // a place whose expert no slot holds (never, unless a wait expired)
-      // poisons the row rather than mixing in the wrong expert
-      const float o = j >= 0 && j < K ? out_l[j][threadIdx.x] : __builtin_nanf("");
+    for (int kk = 0; kk < K; kk++)
       eo = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(
                               __builtin_bit_cast(int, wv), kk)),
-                          o, eo);
-    }
+                          out_l[kk][threadIdx.x], eo);
     const float xr = xadd ? xv + xav : xv;
     x[r] = xr + (out_l[KMAX][threadIdx.x] + eo);
   }

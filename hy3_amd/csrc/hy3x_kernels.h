@@ -47,17 +47,19 @@ __global__ void k_gateup_gemv(const uint8_t *wq, const __half *s16, const int32_
 template <int NT>
 __global__ void k_down_gemv(const uint8_t *wq, const __half *h16, const int32_t *list,
                             const int4 *tiles, const int32_t *n_tiles, float *out);
-struct DecodeSync;
-__global__ void k_decode_gateup(const float *x, const float *xadd, const float *norm_w,
-                                const float *router, const float *bias, int has_bias, int K,
-                                float scale, const uint8_t *wq, const uint8_t *wsh,
-                                DecodeSync sync, float *logits, float *sig, float *score,
-                                int32_t *ids, float *wpre, float *wout, __half *h16,
-                                unsigned long long *stats, unsigned long long *trace,
-                                const float *r_in);
-__global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *spec,
-                              const int32_t *perm, const float *w, int K, float *x,
-                              const float *xadd, const uint8_t *wsh,
+__global__ void k_gateup_decode(const uint8_t *wq, const __half *s16, const float *sig,
+                                const float *score, int K, float scale, int32_t *ids,
+                                float *wpre, float *wout, unsigned long long *stats,
+                                __half *h16, unsigned long long *trace);
+__global__ void k_route_decode(const float *x, const float *xadd, const float *norm_w,
+                               const float *router,
+                               const float *bias, int has_bias, int K, float *logits,
+                               float *sig, float *score, __half *s16, float *s32,
+                               const uint8_t *wq, const uint8_t *wsh, __half *h16,
+                               unsigned long long *trace, const float *r_in);
+__global__ void k_down_decode(const uint8_t *wq, const __half *h16, const int32_t *ids,
+                              const float *w, int K, float *x, const float *xadd,
+                              const uint8_t *wsh,
                               unsigned long long *trace);
 __global__ void k_stream_read(const uint4 *p, int64_t n16, uint32_t *sink);
 __global__ void k_repack_q8x128(const uint8_t *src, uint8_t *dst, int64_t n_super);

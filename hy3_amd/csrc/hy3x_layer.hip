@@ -43,7 +43,6 @@ struct Scratch {
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
   uint32_t *bits = nullptr;  // dispatch: per-expert token bitmaps [E][wt]
-  DecodeSync dsync{};        // single-token path: the first launch's cross-block words
 };
 
 // A scratch allocation and the number of layers using it.
@@ -192,8 +191,7 @@ static constexpr int max_tiles_for(int T, int K, int NT) {
 // max_tokens tokens (slots = tokens x (K_MAX routed + 1 shared)).
 enum ScratchPiece {
   SP_LOGITS, SP_SIG, SP_SCORE, SP_WPRE, SP_W, SP_IDS, SP_S16, SP_S32, SP_S16M, SP_H16M,
-  SP_SSUM, SP_HSUM, SP_H16, SP_OUT, SP_LIST, SP_TILES, SP_NTILES, SP_COUNTS, SP_BITS, SP_SYNC,
-  SP_COUNT
+  SP_SSUM, SP_HSUM, SP_H16, SP_OUT, SP_LIST, SP_TILES, SP_NTILES, SP_COUNTS, SP_BITS, SP_COUNT
 };
 constexpr int bitmap_words(int max_tokens) { return ((max_tokens + 31) / 32 + 3) & ~3; }
 constexpr size_t piece_bytes(int max_tokens, int piece) {
@@ -213,14 +211,10 @@ constexpr size_t piece_bytes(int max_tokens, int piece) {
     case SP_NTILES: return sizeof(int32_t);
     case SP_COUNTS: return (E + 1) * sizeof(int32_t);
     case SP_BITS: return (size_t)E * bitmap_words(max_tokens) * sizeof(uint32_t);
-    case SP_SYNC: return DEC_SYNC_BYTES;
   }
   return 0;
 }
 constexpr size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
-// Device counters of a layer: forwards, experts touched, decode forwards whose
-// routing could not be certified early, expired waits.
-constexpr int kStatWords = 4;
 constexpr size_t scratch_bytes(int max_tokens) {
   size_t off = 0;
   for (int i = 0; i < SP_COUNT; i++) off += align256(piece_bytes(max_tokens, i));
@@ -256,18 +250,6 @@ static Scratch scratch_layout(int max_tokens, uint8_t *base) {
   S.n_tiles = (int32_t *)p[SP_NTILES];
   S.counts = (int32_t *)p[SP_COUNTS];
   S.bits = (uint32_t *)p[SP_BITS];
-  {  // epoch, started[], then the tagged words (8-byte aligned), then spec_ids
-    uint8_t *q = (uint8_t *)p[SP_SYNC];
-    S.dsync.epoch = (uint32_t *)q;
-    S.dsync.started = (uint32_t *)(q + 256);
-    uint64_t *t = (uint64_t *)(q + 256 + DEC_BLOCKS * 4);
-    S.dsync.bound_lo = t;
-    S.dsync.bound_hi = t + E;
-    S.dsync.sig = t + 2 * E;
-    S.dsync.spec = t + 3 * E;
-    S.dsync.spec_ids = (int32_t *)(t + 3 * E + KMAX);
-    S.dsync.perm = S.dsync.spec_ids + KMAX;
-  }
   S.max_tokens = max_tokens;
   S.wt = bitmap_words(max_tokens);
   S.max_tiles = max_tiles_for(max_tokens, KMAX, 1);
@@ -365,14 +347,13 @@ static int create_layer(hy3x_layer **out, int max_tokens, ScratchMem *share) {
       (rc = dalloc(&L->router, (size_t)E * D * sizeof(float))) ||
       (rc = dalloc(&L->bias, E * sizeof(float))) ||
       (!share && (rc = dalloc(&L->scratch_mem->mem, scratch_bytes(max_tokens)))) ||
-      (rc = dalloc(&L->stats, kStatWords * sizeof(unsigned long long)))) {
+      (rc = dalloc(&L->stats, 2 * sizeof(unsigned long long)))) {
     hy3x_layer_destroy(L);
     return rc;
   }
   L->own = scratch_layout(max_tokens, L->scratch_mem->mem);
   if (hipMemset(L->bias, 0, E * sizeof(float)) != hipSuccess ||
-      hipMemset(L->stats, 0, kStatWords * sizeof(unsigned long long)) != hipSuccess ||
-      (!share && hipMemset(L->own.dsync.epoch, 0, DEC_SYNC_BYTES) != hipSuccess)) {
+      hipMemset(L->stats, 0, 2 * sizeof(unsigned long long)) != hipSuccess) {
     hy3x_layer_destroy(L);
     return fail(HY3X_E_HIP, "hipMemset failed");
   }
@@ -505,7 +486,12 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
   float *x = c.x;
   switch (stage) {
     case HY3X_STAGE_ROUTER:
-      if (c.mode == Mode::DECODE) break;  // routing runs inside the gate/up launch
+      if (c.mode == Mode::DECODE) {
+        k_route_decode<<<E + DEC_SH_BLOCKS, 256, 0, st>>>(
+            x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, S.logits, S.sig, S.score,
+            S.s16, S.s32, L->wq, L->shared_q8 ? L->wsh : nullptr, S.h16, L->trace[0], c.r_in);
+        break;
+      }
       // the routing kernels also clear (first kernel) and fill (top-K) the
       // dispatch bitmaps; for T > 8 the RMSNorm kernel stages the MFMA operand
       if (T <= kSmallRouterT) {
@@ -551,10 +537,9 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
       break;
     case HY3X_STAGE_GATEUP:
       if (c.mode == Mode::DECODE)
-        k_decode_gateup<<<DEC_BLOCKS, 256, 0, st>>>(
-            x, c.xadd, L->norm_w, L->router, L->bias, L->has_bias, K, c.scale, L->wq,
-            L->shared_q8 ? L->wsh : nullptr, S.dsync, S.logits, S.sig, S.score, S.ids,
-            S.wpre, S.w, S.h16, L->stats, L->trace[1], c.r_in);
+        k_gateup_decode<<<K * DEC_GU_BLOCKS, 64 * DEC_GU_WAVES, 0, st>>>(L->wq, S.s16, S.sig, S.score, K,
+                                                          c.scale, S.ids, S.wpre, S.w,
+                                                          L->stats, S.h16, L->trace[1]);
       else if (c.mode == Mode::MFMA && c.big)
         mfma_big::k_moe_big<true><<<mt * (F / (16 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
             L->wq, L->shared_q8 ? L->wsh : nullptr, S.s16m, S.ssum, S.list, S.tiles, S.n_tiles, T, K, S.h16m, nullptr);
@@ -575,8 +560,8 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
     case HY3X_STAGE_DOWN:
       if (c.mode == Mode::DECODE)
         k_down_decode<<<D / DEC_DOWN_RPB, 64 * DEC_DOWN_WAVES, 0, st>>>(
-            L->wq, S.h16, S.dsync.spec_ids, S.dsync.perm, S.w, K, x, c.xadd,
-            L->shared_q8 ? L->wsh : nullptr, L->trace[2]);
+            L->wq, S.h16, S.ids, S.w, K, x, c.xadd, L->shared_q8 ? L->wsh : nullptr,
+            L->trace[2]);
       else if (c.mode == Mode::MFMA) {
         k_hsums<<<T * (K + 1), 64, 0, st>>>(S.h16m, S.hsum);
         const uint8_t *wsh = L->shared_q8 ? L->wsh : nullptr;
@@ -679,8 +664,8 @@ static int forward_impl(hy3x_layer *L, const Scratch *sc, const hy3x_layer **own
   c.mt = std::min(max_tiles_for(T, K, c.nt), sc->max_tiles);
   record_stage(L, st, -1);
   for (int stage = HY3X_STAGE_ROUTER; stage <= HY3X_STAGE_COMBINE; stage++) {
-    if (c.mode == Mode::DECODE && stage != HY3X_STAGE_GATEUP && stage != HY3X_STAGE_DOWN)
-      continue;  // decode: routing runs inside the gate/up launch
+    if (c.mode == Mode::DECODE && (stage == HY3X_STAGE_DISPATCH || stage == HY3X_STAGE_COMBINE))
+      continue;
     launch_stage(L, stage, st);
     record_stage(L, st, stage);
   }
@@ -754,18 +739,6 @@ int hy3x_layer_stats(hy3x_layer *L, uint64_t *forwards, uint64_t *experts_touche
   if (forwards) *forwards = h[0];
   if (experts_touched) *experts_touched = h[1];
   if (reset) HIP_TRY(hipMemset(L->stats, 0, sizeof(h)));
-  return HY3X_OK;
-}
-
-int hy3x_layer_decode_stats(hy3x_layer *L, uint64_t *uncertified, uint64_t *expired_waits,
-                            int reset) {
-  if (!L) return fail(HY3X_E_ARG, "NULL layer");
-  unsigned long long h[2];
-  HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemcpy(h, L->stats + 2, sizeof(h), hipMemcpyDeviceToHost));
-  if (uncertified) *uncertified = h[0];
-  if (expired_waits) *expired_waits = h[1];
-  if (reset) HIP_TRY(hipMemset(L->stats + 2, 0, sizeof(h)));
   return HY3X_OK;
 }
 

@@ -60,42 +60,6 @@ __device__ __forceinline__ float tree8_lanes(float c, int v) {
   return __shfl(res, (threadIdx.x & 63) & ~7, 64);
 }
 
-// Chain-transposed LDS rows: buf[v*RS + i] = a[8i+v]. RS = 512 + 4 keeps the
-// eight chains' float4 reads on distinct banks.
-constexpr int NI = D / 8;  // 512 steps per chain
-constexpr int RS = NI + 4;
-
-// The eight fmaf chains of one logit over chain-transposed row pairs (512
-// steps each, i ascending), with their operands in registers spread over a
-// whole wave: lane 8 g + v holds steps [64 g, 64 g + 64) of chain v (64
-// router and 64 s values). The wave runs 8 rounds of 64 FMAs; in round g the
-// lanes of segment g continue chain v from the accumulator the lanes of
-// segment g - 1 left (moved up 8 lanes between rounds); the other lanes'
-// results are discarded. The chain is bound by the dependent FMA latency, and
-// no FMA waits on LDS (8 lanes each running a whole chain from LDS took about
-// 1.5 times as long). Returns chain v's total in lane 56 + v.
-__device__ __forceinline__ float chain_lanes(const float *rs, const float *xs, int lane) {
-  const int v = lane & 7, seg = lane >> 3;
-  float a[64], b[64];
-  const float4 *av = reinterpret_cast<const float4 *>(rs + v * RS + 64 * seg);
-  const float4 *bv = reinterpret_cast<const float4 *>(xs + v * RS + 64 * seg);
-#pragma unroll
-  for (int j = 0; j < 16; j++) {
-    const float4 p = av[j], q = bv[j];
-    a[4 * j] = p.x; a[4 * j + 1] = p.y; a[4 * j + 2] = p.z; a[4 * j + 3] = p.w;
-    b[4 * j] = q.x; b[4 * j + 1] = q.y; b[4 * j + 2] = q.z; b[4 * j + 3] = q.w;
-  }
-  float acc = 0.0f;
-#pragma unroll 1
-  for (int g = 0; g < 8; g++) {
-#pragma unroll
-    for (int j = 0; j < 64; j++) acc = __builtin_fmaf(a[j], b[j], acc);
-    const float up = __shfl_up(acc, 8, 64);
-    if (seg == g + 1) acc = up;
-  }
-  return acc;
-}
-
 // Element m (wave-uniform) of lane l's three-value array, as a wave-uniform
 // value. Each of the three is read out of lane l first and the choice is made
 // between the scalars: a select between the array elements themselves can be

@@ -224,22 +224,11 @@ int hy3x_diag_read_rate(const void *pool, int64_t pool_bytes, int64_t bytes, int
 int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_touched,
                      int reset);
 
-/* Diagnostics of the single-token path (no reference counterpart): the
- * number of decode forwards whose top-K set could not be certified from the
- * early score bounds (their routed gate/up rows waited for the exact top-K;
- * results are the same either way), and of cross-block waits that expired
- * (0 unless something is broken: a forward with an expired wait has wrong
- * results). reset != 0 zeroes both. Synchronises the device. */
-int hy3x_layer_decode_stats(hy3x_layer *layer, uint64_t *uncertified, uint64_t *expired_waits,
-                            int reset);
-
-/* Diagnostics: per-block timestamps of the decode kernels (stage 1: the
- * first launch, router + gate/up, 768 blocks; stage 2: down, 256 blocks;
- * stage 0 is unused). buf: device memory of 8 x 64-bit words per block, or
- * NULL to stop. Each block writes REALTIME-counter (100 MHz) checkpoints:
- * 0 start, 1 s staged, 2 routing known, 3 end; router blocks also 4 score
- * bounds published, 5 exact logit published; block 0 also 6 exact top-K
- * published. */
+/* Diagnostics: per-block timestamps of the decode kernels (stage 0 router,
+ * 1 gate/up, 2 down). buf: device memory of 8 x 64-bit words per block, or
+ * NULL to stop: stage 0 has 576 blocks (192 router logits, then 384 shared
+ * gate/up blocks), stage 1 K x 96, stage 2 256. Each block writes
+ * REALTIME-counter (100 MHz) checkpoints. */
 int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
 
 /* Diagnostics: substitute the RMSNorm scale for ONE forward. The next forward
