@@ -87,10 +87,26 @@ class HY3XError(RuntimeError):
     pass
 
 
+def one_hip_runtime():
+    """Load PyTorch's HIP runtime before anything that links libamdhip64.
+
+    torch ships its own libamdhip64 (soname libamdhip64.so.7) and its
+    libraries ask for it by file name. Loaded first, it also serves
+    libhy3x.so's libamdhip64.so.7 dependency. Loaded after /opt/rocm's copy,
+    the process holds two HIP runtimes, and whichever initialises second
+    finds no device. Without torch, libhy3x.so uses /opt/rocm's runtime alone.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     """Load libhy3x.so (raises if it has not been built)."""
     global _lib
     if _lib is None:
+        one_hip_runtime()
         if not os.path.exists(lib_path):
             raise HY3XError(f"{lib_path} is missing: build it with `python -m hy3_amd.build`")
         h = ctypes.CDLL(lib_path)

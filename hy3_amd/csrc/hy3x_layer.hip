@@ -328,9 +328,10 @@ static int create_layer(hy3x_layer **out, int max_tokens, ScratchMem *share) {
   if (max_tokens < 1 || max_tokens > (1 << 16))
     return fail(HY3X_E_ARG, "max_tokens %d out of range [1, 65536]", max_tokens);
   hy3x_layer *L = new hy3x_layer();
-  if (hipGetDevice(&L->device) != hipSuccess) {
+  const hipError_t gerr = hipGetDevice(&L->device);
+  if (gerr != hipSuccess) {
     delete L;
-    return fail(HY3X_E_HIP, "hipGetDevice failed");
+    return fail(HY3X_E_HIP, "hipGetDevice failed: %s", hipGetErrorString(gerr));
   }
   L->max_tokens = max_tokens;
   if (share) {

@@ -90,10 +90,9 @@ __device__ __forceinline__ void router_block(
     const float *__restrict__ bias, int has_bias, float *__restrict__ logits,
     float *__restrict__ sig, float *__restrict__ score, __half *__restrict__ s16,
     float *__restrict__ s32, unsigned long long *trace, const float *__restrict__ r_in) {
-  __shared__ __attribute__((aligned(16))) float xsf[8 * RS], wsf[8 * RS], rsf[8 * RS];
+  __shared__ __attribute__((aligned(16))) float xsf[8 * RS], rsf[8 * RS];
   const int tid = threadIdx.x;
   trace_point(trace, 0);
-  float r_blk;
   {  // every load in flight at once: 4 float4 of each row per thread
     const float *xt = x + (size_t)t * D, *at = xadd ? xadd + (size_t)t * D : nullptr;
     const float4 *wg = reinterpret_cast<const float4 *>(norm_w);
@@ -108,20 +107,23 @@ __device__ __forceinline__ void router_block(
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int j = 4 * (tid + 256 * u), v = j & 7, i = j >> 3;
-      xsf[(v + 0) * RS + i] = a[u].x; xsf[(v + 1) * RS + i] = a[u].y;
-      xsf[(v + 2) * RS + i] = a[u].z; xsf[(v + 3) * RS + i] = a[u].w;
-      wsf[(v + 0) * RS + i] = b[u].x; wsf[(v + 1) * RS + i] = b[u].y;
-      wsf[(v + 2) * RS + i] = b[u].z; wsf[(v + 3) * RS + i] = b[u].w;
       rsf[(v + 0) * RS + i] = c[u].x; rsf[(v + 1) * RS + i] = c[u].y;
       rsf[(v + 2) * RS + i] = c[u].z; rsf[(v + 3) * RS + i] = c[u].w;
     }
     __shared__ float red_l[4];
-    const float ss = block_sumsq(a, red_l);  // contains the barrier for the LDS rows
-    r_blk = r_in ? r_in[t] : 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
+    const float ss = block_sumsq(a, red_l);  // contains a barrier
+    const float r = r_in ? r_in[t] : 1.0f / __builtin_sqrtf(ss / 4096.0f + 1e-5f);
+    trace_point(trace, 1);
+    // s = (x * norm_w) * r, formed in registers and stored chain-transposed
+    // (norm_w is not staged: the block holds 2 rows in LDS, not 3, so that
+    // three blocks fit a CU)
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int j = 4 * (tid + 256 * u), v = j & 7, i = j >> 3;
+      xsf[(v + 0) * RS + i] = (a[u].x * b[u].x) * r; xsf[(v + 1) * RS + i] = (a[u].y * b[u].y) * r;
+      xsf[(v + 2) * RS + i] = (a[u].z * b[u].z) * r; xsf[(v + 3) * RS + i] = (a[u].w * b[u].w) * r;
+    }
   }
-  trace_point(trace, 1);
-  const float r = r_blk;
-  for (int q = tid; q < 8 * RS; q += 256) xsf[q] = (xsf[q] * wsf[q]) * r;  // s, in place
   __syncthreads();
   if (tid < 64) {  // the eight logit chains in wave 0
     // the chain wave first at its SIMD's issue while the chains run: the shared

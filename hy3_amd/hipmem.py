@@ -10,7 +10,9 @@ _hip = None
 def hip():
     global _hip
     if _hip is None:
-        _hip = ctypes.CDLL("libamdhip64.so")
+        from hy3_amd import one_hip_runtime
+        one_hip_runtime()
+        _hip = ctypes.CDLL("libamdhip64.so.7")
         _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
         _hip.hipMemcpy.restype = ctypes.c_int
         _hip.hipDeviceSynchronize.restype = ctypes.c_int
