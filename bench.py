@@ -68,6 +68,9 @@ def parse():
     p.add_argument("--shared-q8", action="store_true",
                    help="shared expert in hy3's Q8_0, the type real checkpoints carry "
                         "(the configs' default is Q4_K)")
+    p.add_argument("--timeline", type=int, default=0, metavar="FORWARDS",
+                   help="print the per-block timeline of the cold decode launches over FORWARDS "
+                        "forwards (trace checkpoints) and exit")
     p.add_argument("--read-ceiling", action="store_true",
                    help="print the streaming-read rate at the decode and prefill launch sizes "
                         "(the achievable reference for the roofline fractions) and exit")
@@ -344,6 +347,69 @@ def cpu_baseline(torch, H, C, cfg, seconds, shared_q8=False):
                        f"(forward_layer_moe per token), {el:.1f} s")
 
 
+def decode_timeline(torch, forwards):
+    """Per-block timeline of the cold single-token decode (config 0, four
+    resident layers in rotation): every block of the three launches writes
+    REALTIME-counter checkpoints (hy3x_layer_set_trace; 100 MHz); prints, per
+    checkpoint, the median over forwards of the blocks' median / 90th
+    percentile / last time in us from the first route block's start."""
+    import numpy as np
+    import hy3_amd as H
+    from hy3_amd import configs as C
+    torch.cuda.init()
+    cfg = C.CONFIGS[0]
+    layers = []
+    for li in range(4):
+        L = H.MoELayer(1)
+        L.synth_experts(cfg.weight_seed, li)
+        nw, rt, b = C.config_tensors(cfg, li)
+        L.set_router(nw, rt, b)
+        layers.append(L)
+    x = torch.from_numpy(C.inputs(cfg.input_seed, 1).copy()).cuda()
+    # trace buffers: 8 checkpoints per block; stage 0 576 blocks (192 router,
+    # 384 shared rows), stage 1 K x 96 routed gate/up blocks, stage 2 256 down
+    bufs = [torch.zeros(n * 8, dtype=torch.int64, device="cuda") for n in (576, cfg.K * 96, 256)]
+    for i in range(50):
+        layers[i % 4].forward(x.data_ptr(), 1)
+    torch.cuda.synchronize()
+    rows = []
+    for i in range(10 + forwards):
+        L = layers[i % 4]
+        for st, bf in enumerate(bufs):
+            bf.zero_()
+            H._check(H.lib().hy3x_layer_set_trace(L._h, st, bf.data_ptr()))
+        torch.cuda.synchronize()
+        L.forward(x.data_ptr(), 1)
+        torch.cuda.synchronize()
+        for st in range(3):
+            H._check(H.lib().hy3x_layer_set_trace(L._h, st, None))
+        if i < 10:
+            continue
+        r, g, d = (bf.cpu().numpy().reshape(-1, 8).astype(np.float64) for bf in bufs)
+        t0 = r[:, 0].min()
+        us = lambda v: (v - t0) / 100.0
+        rows.append({
+            "route: block start": us(r[:, 0]),
+            "route: router x/row loaded": us(r[:192, 1]),
+            "route: router chains done": us(r[:192, 3]),
+            "route: shared s staged": us(r[192:, 1]),
+            "route: shared rows done": us(r[192:, 3]),
+            "gate/up: block start": us(g[:, 0]),
+            "gate/up: routed, s staged": us(g[:, 1]),
+            "gate/up: rows done": us(g[:, 3]),
+            "down: block start": us(d[:, 0]),
+            "down: rows done": us(d[:, 2]),
+            "down: combine written": us(d[:, 3])})
+    out = []
+    for k in rows[0]:
+        out.append({"checkpoint": k,
+                    "median_us": round(float(np.median([np.median(r[k]) for r in rows])), 2),
+                    "p90_us": round(float(np.median([np.percentile(r[k], 90) for r in rows])), 2),
+                    "last_us": round(float(np.median([r[k].max() for r in rows])), 2)})
+    print(json.dumps({"decode_timeline": out, "forwards": forwards,
+                      "timing": "cold: 4 resident layers in rotation"}), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -353,6 +419,9 @@ def main():
     import torch
     if a.copy_calibration:
         copy_calibration(torch, a.copy_calibration, a.steps)
+        return
+    if a.timeline:
+        decode_timeline(torch, a.timeline)
         return
     if a.read_ceiling:
         import hy3_amd as H
