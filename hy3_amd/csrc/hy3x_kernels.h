@@ -14,26 +14,55 @@ __global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w
                           float *s32,
                           __half *s16m, __half *ssum, int T, uint32_t *bits, int wt,
                           const float *r_in);
-// K chunk of the router GEMM (floats per LDS stage) and chunks in flight
-// (register ring) per tile size: 4 x 8 (tiny), 8 x 16 (mid) and the larger
-// tiles. Few blocks run at small T, so each chunk's load latency must hide
-// behind the previous chunks' FMAs.
-// The largest tile (32 x 32, T > 512) runs 64-wide chunks, four in flight
-// (router stage at 4096 tokens 205 -> 182 us; at 512 tokens, 16 x 16 tiles,
-// the same ring measured 54 -> 60 us, so that tile keeps 128-wide chunks).
-constexpr int ROUTER_KC_TINY = 256, ROUTER_KC_MID = 256, ROUTER_KC_LARGE = 128, ROUTER_KC_XL = 64;
-constexpr int ROUTER_R_TINY = 2, ROUTER_R_MID = 2, ROUTER_R_LARGE = 1, ROUTER_R_XL = 4;
+// Router GEMM tile shapes by token count (k_router_gemm<MT, ME, 4, 8, KC,
+// R>): a thread holds MT x ME (token, expert) outputs of one chain, a block
+// 4 MT tokens x 8 ME experts; K is walked in chunks of KC floats with R
+// chunks in flight. Few blocks run at small T, so there each chunk's load
+// latency must hide behind the previous chunks' FMAs; at large T the tile
+// sets the LDS reads per FMA and the block count per CU. Measured on MI355X
+// (router stage, RMSNorm + GEMM + top-K; the shape replaced in brackets):
+//   TINY  T <= 64:   4 x 8,   KC 256, R 2 (T = 32: 21.4 us; 4 x 16: 25.1, 4 x 24: 31.0)
+//   MID   T <= 256:  8 x 16,  KC 256, R 2 (T = 256: 36.3 us; KC 128: 34.2, 8 x 24: 36.1)
+//   LARGE T <= 1024: 16 x 24, KC 128, R 1 (T = 512: 42.8 us [16 x 16: 49.3],
+//                    T = 1024: 62.4 us [32 x 32: 93.7])
+//   XL    T <= 2048: 32 x 32, KC 64,  R 4 (T = 2048: 108.6 us; 32 x 48: 111.4)
+//   XXL   T > 2048:  32 x 48, KC 64,  R 4 (T = 4096: 155.9 us [32 x 32: 165.7])
+#define HY3X_RCFG(NAME, MT, ME, KC, R)                                                         \
+  constexpr int ROUTER_MT_##NAME = MT, ROUTER_ME_##NAME = ME, ROUTER_KC_##NAME = KC,        \
+                ROUTER_R_##NAME = R;
+#ifndef HY3X_RCFG_TINY
+#define HY3X_RCFG_TINY 1, 1, 256, 2
+#endif
+#ifndef HY3X_RCFG_MID
+#define HY3X_RCFG_MID 2, 2, 256, 2
+#endif
+#ifndef HY3X_RCFG_LARGE
+#define HY3X_RCFG_LARGE 4, 3, 128, 1
+#endif
+#ifndef HY3X_RCFG_XL
+#define HY3X_RCFG_XL 8, 4, 64, 4
+#endif
+#ifndef HY3X_RCFG_XXL
+#define HY3X_RCFG_XXL 8, 6, 64, 4
+#endif
+#define HY3X_RCFG_(NAME, ...) HY3X_RCFG(NAME, __VA_ARGS__)
+HY3X_RCFG_(TINY, HY3X_RCFG_TINY)
+HY3X_RCFG_(MID, HY3X_RCFG_MID)
+HY3X_RCFG_(LARGE, HY3X_RCFG_LARGE)
+HY3X_RCFG_(XL, HY3X_RCFG_XL)
+HY3X_RCFG_(XXL, HY3X_RCFG_XXL)
+#undef HY3X_RCFG_
+#undef HY3X_RCFG
 template <int MT, int ME, int TG, int EG, int KC, int R>
 __global__ __launch_bounds__(256) void k_router_gemm(const float *s32, const float *router, int T,
                                                      float *logits);
-extern template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
-    const float *, const float *, int, float *);
-extern template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_XL, ROUTER_R_XL>(
-    const float *, const float *, int, float *);
-extern template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY>(
-    const float *, const float *, int, float *);
-extern template __global__ void k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
-    const float *, const float *, int, float *);
+#define HY3X_ROUTER_GEMM(NAME)                                                                 \
+  k_router_gemm<ROUTER_MT_##NAME, ROUTER_ME_##NAME, 4, 8, ROUTER_KC_##NAME, ROUTER_R_##NAME>
+extern template __global__ void HY3X_ROUTER_GEMM(TINY)(const float *, const float *, int, float *);
+extern template __global__ void HY3X_ROUTER_GEMM(MID)(const float *, const float *, int, float *);
+extern template __global__ void HY3X_ROUTER_GEMM(LARGE)(const float *, const float *, int, float *);
+extern template __global__ void HY3X_ROUTER_GEMM(XL)(const float *, const float *, int, float *);
+extern template __global__ void HY3X_ROUTER_GEMM(XXL)(const float *, const float *, int, float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
                        int T, int32_t *ids, float *wpre, float *wout, uint32_t *bits, int wt);
 __global__ void k_dispatch_list(const int32_t *ids, int T, int K, int NT, const uint32_t *bits,

@@ -156,15 +156,13 @@ static int dalloc(P **p, size_t bytes) {
 // Up to this many tokens the router runs as one wave per (expert, token);
 // above it as RMSNorm + LDS-tiled GEMM + per-token top-K.
 constexpr int kSmallRouterT = 8;
-// Up to this many tokens the router GEMM uses 4 x 8 block tiles, one output per thread
-// group (the most blocks: at T = 32, 192 of them).
+// Router GEMM tile classes by token count (shapes and measurements with
+// ROUTER_*_TINY ... XXL): TINY up to kTinyRouterT tokens, MID up to
+// kMidRouterT, LARGE up to kLargeRouterT, XL up to kXLRouterT, XXL above.
 constexpr int kTinyRouterT = 64;
-// Up to this many tokens the router GEMM uses 8 x 16 block tiles (more blocks;
-// at T = 256, 41 vs 54 us for the router stage with the next size), then up to
-// kLargeRouterT 16 x 16 tiles (4 x 2 per thread: at T = 512, 384 blocks).
 constexpr int kMidRouterT = 256;
-// Above this many tokens it uses 32 x 32 tiles (8 x 4 per thread: fewer LDS reads per FMA).
-constexpr int kLargeRouterT = 512;
+constexpr int kLargeRouterT = 1024;
+constexpr int kXLRouterT = 2048;
 // From this many tokens the experts run as MFMA grouped GEMMs. Measured on MI355X the
 // MFMA tiles beat the wavefront-reduction GEMV tiles at every T >= 2 (T=2: 51 vs 66 us,
 // T=32: 442 vs 550 us for gate/up + down), so the GEMV tiles only run when selected
@@ -505,18 +503,21 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         k_rmsnorm<<<T, 256, 0, st>>>(x, c.xadd, L->norm_w, mf ? nullptr : S.s16, S.s32,
                                      mf ? S.s16m : nullptr, S.ssum, T, S.bits, S.wt,
                                      c.r_in);
+#define HY3X_LAUNCH_ROUTER(NAME)                                                           \
+  HY3X_ROUTER_GEMM(NAME)<<<dim3((T + 4 * ROUTER_MT_##NAME - 1) / (4 * ROUTER_MT_##NAME),     \
+                                E / (8 * ROUTER_ME_##NAME)),                                  \
+                           256, 0, st>>>(S.s32, L->router, T, S.logits)
         if (T <= kTinyRouterT)
-          k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY><<<dim3((T + 3) / 4, E / 8), 256, 0, st>>>(
-              S.s32, L->router, T, S.logits);
+          HY3X_LAUNCH_ROUTER(TINY);
         else if (T <= kMidRouterT)
-          k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID><<<dim3((T + 7) / 8, E / 16), 256, 0, st>>>(
-              S.s32, L->router, T, S.logits);
+          HY3X_LAUNCH_ROUTER(MID);
         else if (T <= kLargeRouterT)
-          k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE><<<dim3((T + 15) / 16, E / 16), 256, 0, st>>>(
-              S.s32, L->router, T, S.logits);
+          HY3X_LAUNCH_ROUTER(LARGE);
+        else if (T <= kXLRouterT)
+          HY3X_LAUNCH_ROUTER(XL);
         else
-          k_router_gemm<8, 4, 4, 8, ROUTER_KC_XL, ROUTER_R_XL><<<dim3((T + 31) / 32, E / 32), 256, 0, st>>>(
-              S.s32, L->router, T, S.logits);
+          HY3X_LAUNCH_ROUTER(XXL);
+#undef HY3X_LAUNCH_ROUTER
       }
       {
         // one wave per token; up to 256 tokens one wave per block, so that

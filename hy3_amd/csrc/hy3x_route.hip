@@ -387,14 +387,11 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ s
       if (v == 0 && tt < T) logits[(size_t)tt * E + ee] = lg;
     }
 }
-template __global__ void k_router_gemm<8, 4, 4, 8, ROUTER_KC_XL, ROUTER_R_XL>(
-    const float *, const float *, int, float *);
-template __global__ void k_router_gemm<4, 2, 4, 8, ROUTER_KC_LARGE, ROUTER_R_LARGE>(
-    const float *, const float *, int, float *);
-template __global__ void k_router_gemm<2, 2, 4, 8, ROUTER_KC_MID, ROUTER_R_MID>(
-    const float *, const float *, int, float *);
-template __global__ void k_router_gemm<1, 1, 4, 8, ROUTER_KC_TINY, ROUTER_R_TINY>(
-    const float *, const float *, int, float *);
+template __global__ void HY3X_ROUTER_GEMM(TINY)(const float *, const float *, int, float *);
+template __global__ void HY3X_ROUTER_GEMM(MID)(const float *, const float *, int, float *);
+template __global__ void HY3X_ROUTER_GEMM(LARGE)(const float *, const float *, int, float *);
+template __global__ void HY3X_ROUTER_GEMM(XL)(const float *, const float *, int, float *);
+template __global__ void HY3X_ROUTER_GEMM(XXL)(const float *, const float *, int, float *);
 
 // Routing of one token per wave (T > 1 paths), a block holding 1 or 4 waves: sigmoid and
 // score of the 192 logits (expert lane + 64 m in slot m), the top-K in
