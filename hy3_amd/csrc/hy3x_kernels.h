@@ -22,11 +22,14 @@ __global__ void k_rmsnorm(const float *x, const float *xadd, const float *norm_w
 // sets the LDS reads per FMA and the block count per CU. Measured on MI355X
 // (router stage, RMSNorm + GEMM + top-K; the shape replaced in brackets):
 //   TINY  T <= 64:   4 x 8,   KC 256, R 2 (T = 32: 21.4 us; 4 x 16: 25.1, 4 x 24: 31.0)
-//   MID   T <= 256:  8 x 16,  KC 256, R 2 (T = 256: 36.3 us; KC 128: 34.2, 8 x 24: 36.1)
-//   LARGE T <= 1024: 16 x 24, KC 128, R 1 (T = 512: 42.8 us [16 x 16: 49.3],
-//                    T = 1024: 62.4 us [32 x 32: 93.7])
-//   XL    T <= 2048: 32 x 32, KC 64,  R 4 (T = 2048: 108.6 us; 32 x 48: 111.4)
-//   XXL   T > 2048:  32 x 48, KC 64,  R 4 (T = 4096: 155.9 us [32 x 32: 165.7])
+//   MID   T <= 256:  8 x 16,  KC 256, R 2 (T = 96 / 160 / 256: 28.5 / 28.8 / 36.4 us;
+//                    KC 128: 29.5 / 29.6 / 34.3, 8 x 24: 33.7 / 33.9 / 34.5)
+//   LARGE T <= 1536: 16 x 24, KC 128, R 1 (T = 512: 42.8 us [16 x 16: 49.3],
+//                    T = 1024: 62.4 us [32 x 32: 93.7], T = 1536: 86.3 [103.0];
+//                    T = 2048: 113.7 against 108.6 for 32 x 32)
+//   XL    T <= 2560: 32 x 32, KC 64,  R 4 (T = 2560: 115.0 us; 32 x 48: 138.5)
+//   XXL   T > 2560:  32 x 48, KC 64,  R 4 (T = 3072: 140.9 us [32 x 32: 147.2],
+//                    T = 4096: 155.9 [165.7])
 #define HY3X_RCFG(NAME, MT, ME, KC, R)                                                         \
   constexpr int ROUTER_MT_##NAME = MT, ROUTER_ME_##NAME = ME, ROUTER_KC_##NAME = KC,        \
                 ROUTER_R_##NAME = R;

@@ -159,10 +159,14 @@ constexpr int kSmallRouterT = 8;
 // Router GEMM tile classes by token count (shapes and measurements with
 // ROUTER_*_TINY ... XXL): TINY up to kTinyRouterT tokens, MID up to
 // kMidRouterT, LARGE up to kLargeRouterT, XL up to kXLRouterT, XXL above.
-constexpr int kTinyRouterT = 64;
-constexpr int kMidRouterT = 256;
-constexpr int kLargeRouterT = 1024;
-constexpr int kXLRouterT = 2048;
+#ifndef HY3X_ROUTER_CLASS_T
+#define HY3X_ROUTER_CLASS_T 64, 256, 1536, 2560
+#endif
+constexpr int kRouterClassT[4] = {HY3X_ROUTER_CLASS_T};
+constexpr int kTinyRouterT = kRouterClassT[0];
+constexpr int kMidRouterT = kRouterClassT[1];
+constexpr int kLargeRouterT = kRouterClassT[2];
+constexpr int kXLRouterT = kRouterClassT[3];
 // From this many tokens the experts run as MFMA grouped GEMMs. Measured on MI355X the
 // MFMA tiles beat the wavefront-reduction GEMV tiles at every T >= 2 (T=2: 51 vs 66 us,
 // T=32: 442 vs 550 us for gate/up + down), so the GEMV tiles only run when selected

@@ -152,11 +152,11 @@ def test_routing_top_k_variants(torch, layer, cpu, K, T):
 
 
 @pytest.mark.parametrize("T,K", [(64, 8), (65, 8), (256, 8), (257, 3), (512, 8), (513, 5),
-                                 (1024, 8), (1025, 6), (2048, 8), (2049, 4)])
+                                 (1536, 8), (1537, 6), (2560, 8), (2561, 4)])
 def test_routing_at_router_tile_boundaries(torch, layer, cpu, T, K):
     """Every token's routing at both sides of each change of router GEMM tile
-    (64 / 256 / 1024 / 2048 tokens) and of the top-K launch shape (256 tokens),
-    with the tile edges falling mid-tile (65, 257, 513, 1025, 2049)."""
+    (64 / 256 / 1536 / 2560 tokens) and of the top-K launch shape (256 tokens),
+    with the tile edges falling mid-tile (65, 257, 513, 1537, 2561)."""
     x = C.inputs(0xC3, T, first_token=1000)
     _, ids, wpre, w = run(torch, layer, x, K)
     r = cpu.route(x, K)
