@@ -364,7 +364,11 @@ __global__ __launch_bounds__(B_THREADS) void k_moe_big(
   using C = Cfg<GATEUP>;
   const int nreal = *n_tiles * C::NRT;
   if ((int)blockIdx.x >= nreal) return;
-  const int w = xcd_remap(blockIdx.x, nreal);
+  // gate/up: consecutive work items (the row tiles of one token tile) on one
+  // XCD, sharing the tile's activations in its L2; down: dealt round-robin,
+  // as the workgroups are (measured at 4096 tokens, Zipf routing: down 757
+  // -> 740 us round-robin; gate/up 1284 -> 1329 us, so it keeps the runs)
+  const int w = GATEUP ? xcd_remap(blockIdx.x, nreal) : (int)blockIdx.x;
   const int tile = w / C::NRT, rt = w % C::NRT;
   const int4 td = tiles[tile];
   const int e = td.x, o = td.y, n = td.z;
