@@ -110,6 +110,9 @@ extern template __global__ void k_down_gemv<1>(const uint8_t *, const __half *, 
 extern template __global__ void k_down_gemv<4>(const uint8_t *, const __half *, const int32_t *,
                                                const int4 *, const int32_t *, float *);
 
+// Tiles of grid margin for the kernels that deal whole tiles round-robin to
+// the XCDs (xcd_tile_rr, hy3x_mfma_ops.h).
+constexpr int XCD_TILE_RR_MARGIN = 7;
 // The MFMA grouped GEMMs in two shapes (hy3x_mfma.hip, compiled once per
 // shape). A work tile has ROWS_GU = 16 WAVES RGU gate/up rows (per matrix) or
 // twice as many down rows and up to TOKENS tokens; each wave takes 16 RGU

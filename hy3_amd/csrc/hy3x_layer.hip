@@ -547,7 +547,7 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
                                                           c.scale, S.ids, S.wpre, S.w,
                                                           L->stats, S.h16, L->trace[1]);
       else if (c.mode == Mode::MFMA && c.big)
-        mfma_big::k_moe_big<true><<<mt * (F / (16 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
+        mfma_big::k_moe_big<true><<<(mt + XCD_TILE_RR_MARGIN) * (F / (16 * BIG_WAVES)), 64 * BIG_WAVES, 0, st>>>(
             L->wq, L->shared_q8 ? L->wsh : nullptr, S.s16m, S.ssum, S.list, S.tiles, S.n_tiles, T, K, S.h16m, nullptr);
       else if (c.mode == Mode::MFMA && c.wide)
         mfma_wide::k_moe_mfma<true>

@@ -565,6 +565,9 @@ __global__ __launch_bounds__(MT_THREADS) void k_moe_mfma(
   // this forward's work leave at once, and the work items are dealt over the
   // real blocks only, so that every XCD gets an even share.
   const int nreal = *n_tiles * C::NRT;
+  // each XCD on a contiguous run of the work (the token tiles of an expert
+  // share its weights in L2; whole tiles dealt round-robin measured equal at
+  // 32 tokens and 0.7 % slower at 512)
   if ((int)blockIdx.x >= nreal) return;
   const int w = xcd_remap(blockIdx.x, nreal);
   const int tile = w / C::NRT, rt = w % C::NRT;

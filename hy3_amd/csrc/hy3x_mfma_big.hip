@@ -363,12 +363,19 @@ __global__ __launch_bounds__(B_THREADS) void k_moe_big(
     __half *__restrict__ h16m, float *__restrict__ out) {
   using C = Cfg<GATEUP>;
   const int nreal = *n_tiles * C::NRT;
-  if ((int)blockIdx.x >= nreal) return;
-  // gate/up: consecutive work items (the row tiles of one token tile) on one
-  // XCD, sharing the tile's activations in its L2; down: dealt round-robin,
-  // as the workgroups are (measured at 4096 tokens, Zipf routing: down 757
-  // -> 740 us round-robin; gate/up 1284 -> 1329 us, so it keeps the runs)
-  const int w = GATEUP ? xcd_remap(blockIdx.x, nreal) : (int)blockIdx.x;
+  // gate/up: whole tiles dealt round-robin to the XCDs, a tile's row tiles
+  // consecutive on one (sharing its activations in L2; the grid carries
+  // XCD_TILE_RR_MARGIN tiles of margin); down: work items round-robin, as the
+  // workgroups are. Measured at 4096 tokens, Zipf routing, against one
+  // contiguous run of work per XCD: gate/up 1320 -> 1297 and 1296 -> 1268 us
+  // (items round-robin: 1329), down 757 -> 740 us (tiles round-robin: 764).
+  int w;
+  if constexpr (GATEUP) {
+    w = xcd_tile_rr(blockIdx.x, C::NRT);
+  } else {
+    w = blockIdx.x;
+  }
+  if (w >= nreal) return;
   const int tile = w / C::NRT, rt = w % C::NRT;
   const int4 td = tiles[tile];
   const int e = td.x, o = td.y, n = td.z;

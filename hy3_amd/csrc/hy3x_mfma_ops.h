@@ -94,6 +94,18 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return x * q + (x < r ? x : r) + i;
 }
 
+// Launch order -> work item with whole tiles dealt round-robin to the XCDs:
+// tile j's nrt row tiles run consecutively on XCD j % 8 (sharing the tile's
+// activations in that L2), and neighbouring tiles go to different XCDs. Work
+// item w < n_tiles * nrt is block ((w / nrt / 8) * nrt + w % nrt) * 8 +
+// (w / nrt) % 8, which is below (n_tiles + 7) * nrt: the grid needs
+// XCD_TILE_RR_MARGIN = 7 tiles of margin; blocks whose item is past the work
+// leave.
+__device__ __forceinline__ int xcd_tile_rr(int bid, int nrt) {
+  const int x = bid & 7, i = bid >> 3;
+  return ((i / nrt) * 8 + x) * nrt + i % nrt;
+}
+
 // fp16 weights (exact q) of 8 consecutive bytes, in the staged activations'
 // run order (0, 2, 1, 3, 4, 6, 5, 7).
 __device__ __forceinline__ h8_t q8_run(u2_t b) {
