@@ -180,9 +180,10 @@ constexpr int kMfmaMinT = 2;
 constexpr int kMfmaWideMinT = 384;
 // From this many tokens the MFMA GEMMs use 128-token tiles
 // (mfma_big). Measured on MI355X (ms per layer, wide vs 128-token tiles):
-// 1024 tokens 0.93 vs 0.97, 2048: 1.49 vs 1.41, 3072: 2.05 vs 1.97, 4096: 2.60
+// 1024 tokens 0.923 vs 0.928, 1152: 1.002 vs 0.984, 1280: 1.047 vs 1.037,
+// 1536: 1.222 vs 1.179, 2048: 1.489 vs 1.417, 3072: 2.05 vs 1.97, 4096: 2.60
 // vs 2.46, 4096 with Zipf routing: 2.58 vs 2.34-2.38.
-constexpr int kMfmaBigMinT = 2048;
+constexpr int kMfmaBigMinT = 1152;
 
 static constexpr int max_tiles_for(int T, int K, int NT) {
   const int n = T * K;
