@@ -174,10 +174,11 @@ constexpr int kXLRouterT = kRouterClassT[3];
 constexpr int kMfmaMinT = 2;
 // From this many tokens the MFMA GEMMs use the wide tile shape (64 tokens, 8 waves).
 // Measured on MI355X (ms per layer, narrow vs wide): 32 tokens 0.32 vs 0.37,
-// 128: 0.43 vs 0.48, 256: 0.51 vs 0.56, 384: 0.60 vs 0.60, 512: 0.69 vs 0.65,
-// 4096 (Zipf routing): 3.36 vs 2.62 -- with few tokens per expert the tiles are
-// mostly empty and one workgroup per CU hides less latency than two.
-constexpr int kMfmaWideMinT = 384;
+// 128: 0.43 vs 0.48, 256: 0.503 vs 0.517, 320: 0.556 vs 0.554, 384: 0.598 vs
+// 0.585, 448: 0.642 vs 0.607, 512: 0.69 vs 0.65, 4096 (Zipf routing): 3.36 vs
+// 2.62 -- with few tokens per expert the tiles are mostly empty and one
+// workgroup per CU hides less latency than two.
+constexpr int kMfmaWideMinT = 320;
 // From this many tokens the MFMA GEMMs use 128-token tiles
 // (mfma_big). Measured on MI355X (ms per layer, wide vs 128-token tiles):
 // 1024 tokens 0.923 vs 0.928, 1152: 1.002 vs 0.984, 1280: 1.047 vs 1.037,

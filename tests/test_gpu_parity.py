@@ -436,11 +436,11 @@ def test_expert_paths_match_oracle(torch, layer, cpu, T):
     3 / 4 its narrow / wide tile shape, 5 its 128-token tiles) meets the tolerance on the same
     tokens; routing is identical on all; hy3x_layer_last_path reports the
     path that ran (automatic: decode kernels at T = 1, the narrow MFMA shape
-    below 384 tokens, the wide one from there, 128-token tiles from 1152)."""
+    below 320 tokens, the wide one from there, 128-token tiles from 1152)."""
     x = C.inputs(0xC2, T, first_token=300)
     rows = np.linspace(0, T - 1, min(T, 6)).astype(int)
     yo, ro = cpu.forward(x[rows])
-    mfma_auto = 5 if T >= 1152 else 4 if T >= 384 else 3
+    mfma_auto = 5 if T >= 1152 else 4 if T >= 320 else 3
     ran = {0: 0 if T == 1 else mfma_auto, 1: 1, 2: mfma_auto, 3: 3, 4: 4, 5: 5}
     try:
         for path in (0, 1, 2, 3, 4, 5):
@@ -699,7 +699,7 @@ def test_q8_shared_big_tiles_equal_narrow_tiles(torch, q8_layer, T):
         assert q8_layer.last_path() == 5
         q8_layer.set_path(0)
         y0 = run(torch, q8_layer, x)[0]
-        assert q8_layer.last_path() == (5 if T >= 1152 else 4 if T >= 384 else 3)
+        assert q8_layer.last_path() == (5 if T >= 1152 else 4 if T >= 320 else 3)
     finally:
         q8_layer.set_path(0)
     assert np.array_equal(y3.view(np.uint32), y5.view(np.uint32))
