@@ -121,13 +121,15 @@ __device__ __forceinline__ void down_rows(const uint8_t *__restrict__ wq, Expert
 // figures are recorded with the design notes, not as build switches).
 constexpr int DEC_RPW = 4;                   // gate/up rows per wave
 constexpr int DEC_GU_PF = 2;                 // gate/up rows in flight per wave (4: all of them, 0.3-0.4 us slower)
-// Shared gate/up rows per wave of a routing block: one, so that the shared
-// blocks (384 of 4 rows) finish before the router chains do (with 16-row
-// blocks the last ones ended about 1 us after the chains; C0 32.4 -> 31.5 us).
-constexpr int DEC_SH_RPW = 1;
+// Shared gate/up rows per wave of a routing block: two (192 blocks of 8
+// rows; each block recomputes s, so fewer blocks also load x and norm_w
+// fewer times). C0 per forward, 1 / 2 / 3 / 4 rows per wave: 30.06 / 29.87 /
+// 30.7 / 31.3 us (with 16-row blocks and the route blocks' LDS larger, the
+// last shared blocks had ended about 1 us after the router chains).
+constexpr int DEC_SH_RPW = 2;
 constexpr int DEC_RPB = 4 * DEC_SH_RPW;       // shared gate/up rows per routing block (four waves)
 static_assert(F % DEC_RPB == 0, "the routing kernel's shared blocks cover every row");
-constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (384)
+constexpr int DEC_SH_BLOCKS = F / DEC_RPB;   // shared gate/up blocks of the routing kernel (192)
 // Waves per routed gate/up block (each block routes the token once, then its
 // waves stream DEC_RPW rows each).
 constexpr int DEC_GU_WAVES = 4;
