@@ -367,10 +367,10 @@ def decode_timeline(torch, forwards):
         layers.append(L)
     x = torch.from_numpy(C.inputs(cfg.input_seed, 1).copy()).cuda()
     # trace buffers: 8 checkpoints per block; stage 0 384 blocks (192 router,
-    # 192 of shared rows), stage 1 K x 96 routed gate/up blocks, stage 2 256
+    # 192 of shared rows), stage 1 K x 384 routed gate/up blocks, stage 2 256
     # down (sized with room to spare; blocks that did not run stay zero and
     # are dropped)
-    bufs = [torch.zeros(n * 8, dtype=torch.int64, device="cuda") for n in (1024, cfg.K * 96, 256)]
+    bufs = [torch.zeros(n * 8, dtype=torch.int64, device="cuda") for n in (1024, 8192, 1024)]
     for i in range(50):
         layers[i % 4].forward(x.data_ptr(), 1)
     torch.cuda.synchronize()
@@ -388,7 +388,7 @@ def decode_timeline(torch, forwards):
         if i < 10:
             continue
         r, g, d = (bf.cpu().numpy().reshape(-1, 8).astype(np.float64) for bf in bufs)
-        r = r[r[:, 0] > 0]
+        r, g, d = (a[a[:, 0] > 0] for a in (r, g, d))
         t0 = r[:, 0].min()
         us = lambda v: (v - t0) / 100.0
         rows.append({

@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void k_down_gemv(const uint8_t *__restrict__ w
 // slot K the shared expert; the expert id is one load away from the weights.
 
 // Routed gate/up of a single token: block = DEC_GU_RPB rows (DEC_GU_WAVES
-// waves x 4) of routed slot blockIdx.x / DEC_GU_BLOCKS. Every wave routes the
+// waves x DEC_RPW) of routed slot blockIdx.x / DEC_GU_BLOCKS. Every wave routes the
 // token itself from the 192 sigmoid values / scores (the routing contract,
 // identical in every wave and block: topk_wave_fast, or topk_wave_regs on a
 // tie) and takes the expert of its slot; block 0 publishes the routing and
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_gateup_decode(
   trace_point(trace, 0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = blockIdx.x / DEC_GU_BLOCKS, rc = blockIdx.x % DEC_GU_BLOCKS;
-  // the token's staged s, once per block (the four waves read it from LDS),
+  // the token's staged s, once per block (the block's waves read it from LDS),
   // loaded together with the routing inputs
   const int tid = threadIdx.x;
   constexpr int NT = 64 * DEC_GU_WAVES, NS = (D / 8 + NT - 1) / NT;  // 16-byte pieces per thread

@@ -227,7 +227,7 @@ int hy3x_layer_stats(hy3x_layer *layer, uint64_t *forwards, uint64_t *experts_to
 /* Diagnostics: per-block timestamps of the decode kernels (stage 0 router,
  * 1 gate/up, 2 down). buf: device memory of 8 x 64-bit words per block, or
  * NULL to stop: stage 0 has 384 blocks (192 router logits, then 192 shared
- * gate/up blocks), stage 1 K x 96, stage 2 256. Each block writes
+ * gate/up blocks), stage 1 K x 384, stage 2 256. Each block writes
  * REALTIME-counter (100 MHz) checkpoints. */
 int hy3x_layer_set_trace(hy3x_layer *layer, int stage, void *buf);
 
