@@ -67,8 +67,9 @@ extern template __global__ void HY3X_ROUTER_GEMM(LARGE)(const float *, const flo
 extern template __global__ void HY3X_ROUTER_GEMM(XL)(const float *, const float *, int, float *);
 extern template __global__ void HY3X_ROUTER_GEMM(XXL)(const float *, const float *, int, float *);
 __global__ void k_topk(const float *logits, const float *bias, int has_bias, int K, float scale,
-                       int T, int32_t *ids, float *wpre, float *wout, uint32_t *bits, int wt);
-__global__ void k_dispatch_list(const int32_t *ids, int T, int K, int NT, const uint32_t *bits,
+                       int T, int32_t *ids, float *wpre, float *wout, uint32_t *bits, int wt,
+                       uint8_t *ranks);
+__global__ void k_dispatch_list(const uint8_t *ranks, int T, int K, int NT, const uint32_t *bits,
                                 int wt, int32_t *list, int4 *tiles,
                                 int32_t *n_tiles, int max_tiles, int32_t *counts_out,
                                 unsigned long long *stats);

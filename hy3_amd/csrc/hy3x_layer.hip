@@ -43,6 +43,7 @@ struct Scratch {
   int32_t *ids = nullptr, *list = nullptr, *n_tiles = nullptr, *counts = nullptr;
   int4 *tiles = nullptr;
   uint32_t *bits = nullptr;  // dispatch: per-expert token bitmaps [E][wt]
+  uint8_t *ranks = nullptr;  // dispatch: [E][32 wt] token t's place of expert e where t's bit is set
 };
 
 // A scratch allocation and the number of layers using it.
@@ -195,7 +196,8 @@ static constexpr int max_tiles_for(int T, int K, int NT) {
 // max_tokens tokens (slots = tokens x (K_MAX routed + 1 shared)).
 enum ScratchPiece {
   SP_LOGITS, SP_SIG, SP_SCORE, SP_WPRE, SP_W, SP_IDS, SP_S16, SP_S32, SP_S16M, SP_H16M,
-  SP_SSUM, SP_HSUM, SP_H16, SP_OUT, SP_LIST, SP_TILES, SP_NTILES, SP_COUNTS, SP_BITS, SP_COUNT
+  SP_SSUM, SP_HSUM, SP_H16, SP_OUT, SP_LIST, SP_TILES, SP_NTILES, SP_COUNTS, SP_BITS, SP_RANKS,
+  SP_COUNT
 };
 constexpr int bitmap_words(int max_tokens) { return ((max_tokens + 31) / 32 + 3) & ~3; }
 constexpr size_t piece_bytes(int max_tokens, int piece) {
@@ -215,6 +217,7 @@ constexpr size_t piece_bytes(int max_tokens, int piece) {
     case SP_NTILES: return sizeof(int32_t);
     case SP_COUNTS: return (E + 1) * sizeof(int32_t);
     case SP_BITS: return (size_t)E * bitmap_words(max_tokens) * sizeof(uint32_t);
+    case SP_RANKS: return (size_t)E * bitmap_words(max_tokens) * 32;
   }
   return 0;
 }
@@ -254,6 +257,7 @@ static Scratch scratch_layout(int max_tokens, uint8_t *base) {
   S.n_tiles = (int32_t *)p[SP_NTILES];
   S.counts = (int32_t *)p[SP_COUNTS];
   S.bits = (uint32_t *)p[SP_BITS];
+  S.ranks = (uint8_t *)p[SP_RANKS];
   S.max_tokens = max_tokens;
   S.wt = bitmap_words(max_tokens);
   S.max_tiles = max_tiles_for(max_tokens, KMAX, 1);
@@ -531,14 +535,14 @@ static void launch_stage(hy3x_layer *L, int stage, hipStream_t st) {
         const int wpb = T <= 256 ? 1 : 4;
         k_topk<<<(T + wpb - 1) / wpb, 64 * wpb, 0, st>>>(S.logits, L->bias, L->has_bias, K,
                                                          c.scale, T, S.ids, S.wpre, S.w,
-                                                         S.bits, S.wt);
+                                                         S.bits, S.wt, S.ranks);
       }
       break;
     case HY3X_STAGE_DISPATCH:
       if (c.mode == Mode::MFMA && T <= kSmallRouterT)
         k_stage_mfma<<<T, 256, 0, st>>>(S.s32, S.s16m, S.ssum);
       if (c.mode != Mode::DECODE) {
-        k_dispatch_list<<<E + 1, 256, 0, st>>>(S.ids, T, K, c.nt, S.bits, S.wt,
+        k_dispatch_list<<<E + 1, 256, 0, st>>>(S.ranks, T, K, c.nt, S.bits, S.wt,
                                                S.list, S.tiles, S.n_tiles, mt, S.counts,
                                                L->stats);
       }

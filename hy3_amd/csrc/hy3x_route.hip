@@ -401,7 +401,8 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
                                               const float *__restrict__ bias, int has_bias, int K,
                                               float scale, int T, int32_t *__restrict__ ids,
                                               float *__restrict__ wpre, float *__restrict__ wout,
-                                              uint32_t *__restrict__ bits, int wt) {
+                                              uint32_t *__restrict__ bits, int wt,
+                                              uint8_t *__restrict__ ranks) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -428,7 +429,10 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
     topk_wave_regs(sc, sg, K, scale, ids_t, wpre + (size_t)t * K, wout + (size_t)t * K);
     my_e = lane < K ? ids_t[lane] : 0;  // this lane's own store: program order
   }
-  if (bits && lane < K) atomicOr(&bits[(size_t)my_e * wt + (t >> 5)], 1u << (t & 31));
+  if (bits && lane < K) {
+    atomicOr(&bits[(size_t)my_e * wt + (t >> 5)], 1u << (t & 31));
+    ranks[(size_t)my_e * wt * 32 + t] = (uint8_t)lane;  // lane k holds place k
+  }
 }
 
 // Device dispatch: per-expert slot lists and the work-tile list.
@@ -458,7 +462,7 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int *tmp) {
 // tiles, and its slots in token order from its bitmap (popcount prefix sums).
 // Block E also writes the tile count, the per-expert counts and the stats.
 __global__ __launch_bounds__(256) void k_dispatch_list(
-    const int32_t *__restrict__ ids, int T, int K, int NT, const uint32_t *__restrict__ bits,
+    const uint8_t *__restrict__ ranks, int T, int K, int NT, const uint32_t *__restrict__ bits,
     int wt, int32_t *__restrict__ list,
     int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles, int max_tiles,
     int32_t *__restrict__ counts_out, unsigned long long *__restrict__ stats) {
@@ -508,22 +512,27 @@ __global__ __launch_bounds__(256) void k_dispatch_list(
   for (int w0 = 0; w0 < nw; w0 += 256) {  // rounds of 256 bitmap words, in order
     const int w = w0 + tid;
     uint32_t word = w < nw ? bits[(size_t)e * wt + w] : 0u;
+    // the word's 32 tokens' places of e (k_topk's rank bytes; read only where
+    // the bit is set), in two 16-byte loads issued with the bitmap word's
+    uint4 rk[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (word) {
+      const uint4 *rp = reinterpret_cast<const uint4 *>(ranks + (size_t)e * wt * 32 + 32 * w);
+      rk[0] = rp[0];
+      rk[1] = rp[1];
+    }
     const int pos = base + block_exclusive_scan256(__popc(word), tmp);
     int r = 0;
     while (word) {
       const int b = __ffs(word) - 1;
       word &= word - 1u;
       const int t = 32 * w + b;
-      // the rank of e among t's ids (K - 1 when no earlier one matches): all
-      // loads issued at once, the first match kept
-      int idv[KMAX - 1];
-#pragma unroll
-      for (int kk = 0; kk < KMAX - 1; kk++)  // clamped: a valid address for any K
-        idv[kk] = ids[(size_t)t * K + (kk < K ? kk : K - 1)];
-      int k = K - 1;
-#pragma unroll
-      for (int kk = KMAX - 2; kk >= 0; kk--)
-        if (kk < K - 1 && idv[kk] == e) k = kk;
+      // byte b of the 32 (a select chain: an indexed read of a register
+      // array would go through scratch memory)
+      const int q = b >> 2;
+      const uint4 h = q < 4 ? rk[0] : rk[1];
+      const int qq = q & 3;
+      const uint32_t wsel = qq == 0 ? h.x : qq == 1 ? h.y : qq == 2 ? h.z : h.w;
+      const int k = (int)((wsel >> (8 * (b & 3))) & 0xffu);
       list[eoff + pos + r] = t * K + k;
       r++;
     }
