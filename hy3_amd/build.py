@@ -36,14 +36,19 @@ FLAGS = [
 ]
 
 
-# Per-source additions: the narrow and wide MFMA tile kernels schedule with
-# LLVM's iterative-ILP strategy (measured: 512 tokens gate/up 350.1 -> 347.6
-# us, down 200.6 -> 198.3; 32 tokens 164.1 -> 163.1 and 95.5 -> 94.7; the
-# 128-token tiles and the decode kernels measured slower with it: 1250 ->
-# 1336 us, 29.3 -> 30.1 us, so they keep the default scheduler).
+# Per-source additions: the narrow and wide MFMA tile kernels and the
+# single-token router launch schedule with LLVM's iterative-ILP strategy
+# (measured: 512 tokens gate/up 350.1 -> 347.6 us, down 200.6 -> 198.3; 32
+# tokens 164.1 -> 163.1 and 95.5 -> 94.7; decode 29.30 -> 29.06 us with the
+# router launch alone). The 128-token tiles, the decode expert kernels and
+# the multi-token router measured slower with it (1250 -> 1336 us; 29.3 ->
+# 30.4 us; router stage at 512 tokens 42.8 -> 45.3 us), so they keep the
+# default scheduler.
+ILP = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
 FILE_FLAGS = {
-    "hy3x_mfma.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
-    "hy3x_mfma_wide.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "hy3x_mfma.hip": ILP,
+    "hy3x_mfma_wide.hip": ILP,
+    "hy3x_route_decode.hip": ILP,
 }
 
 
