@@ -44,11 +44,15 @@ FLAGS = [
 # the multi-token router measured slower with it (1250 -> 1336 us; 29.3 ->
 # 30.4 us; router stage at 512 tokens 42.8 -> 45.3 us), so they keep the
 # default scheduler.
+# The decode expert kernels (hy3x_gemv.hip) schedule with the AMDGPU
+# register-pressure trackers (decode 29.41 -> 29.26 us; other scheduler
+# strategies, larger memory clauses and wave priorities measured slower).
 ILP = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
 FILE_FLAGS = {
     "hy3x_mfma.hip": ILP,
     "hy3x_mfma_wide.hip": ILP,
     "hy3x_route_decode.hip": ILP,
+    "hy3x_gemv.hip": ["-mllvm", "-amdgpu-use-amdgpu-trackers"],
 }
 
 
