@@ -511,7 +511,7 @@ def test_non_finite_bias(torch, layer, cpu, T):
         cpu.bias = saved
 
 
-@pytest.mark.parametrize("T", [2, 40, 333, 1000, 4096])
+@pytest.mark.parametrize("T", [2, 40, 333, 1000, 1200, 4096])
 def test_big_tiles_equal_narrow_tiles(torch, layer, cpu, T):
     """The 128-token tiles (activations staged per half block column, the
     dequantised weights reused over up to eight 16-token groups) do per
