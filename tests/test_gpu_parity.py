@@ -165,6 +165,23 @@ def test_routing_at_router_tile_boundaries(torch, layer, cpu, T, K):
     assert np.array_equal(w.view(np.uint32), r["w"].view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [319, 320, 1151, 1152])
+def test_default_path_thresholds(torch, layer, cpu, T):
+    """At both sides of the default path's changes of tile shape (narrow to
+    wide tiles at 320 tokens, wide to 128-token tiles at 1152): the layer
+    reports the shape it ran, routing is bit-exact and sampled outputs match
+    the oracle."""
+    x = C.inputs(0xC9, T, first_token=2000)
+    y, ids, wpre, _ = run(torch, layer, x)
+    assert layer.last_path() == (5 if T >= 1152 else 4 if T >= 320 else 3)
+    r = cpu.route(x)
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(wpre.view(np.uint32), r["wpre"].view(np.uint32))
+    rows = np.linspace(0, T - 1, 4).astype(int)
+    yo, _ = cpu.forward(x[rows])
+    assert O.rel_l2(y[rows] - x[rows], yo - x[rows]) <= TOL
+
+
 def test_routing_without_bias(torch, layer, cpu):
     set_bias(layer, cpu, "none")
     x = C.inputs(0xC1, 12)
@@ -530,14 +547,15 @@ def test_big_tiles_equal_narrow_tiles(torch, layer, cpu, T):
     assert np.array_equal(y3.view(np.uint32), y5.view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [40, 129, 200, 257])
+@pytest.mark.parametrize("T", [16, 40, 64, 128, 129, 200, 257])
 def test_mfma_tile_shapes_on_crowded_experts(torch, layer, cpu, T):
     """A bias of +50 on eight experts sends every token to them, so each of
     those experts holds all T tokens: the narrow shape (32-token tiles), the
     wide one (64-token tiles: T = 40 is one tile of 40 tokens, three 16-token
     column groups; T = 200 is three full tiles of four groups and one of 8
     tokens) and the 128-token tiles (T = 129 and 257: full tiles plus a tile of
-    one token) give the same output bit for bit (the same per-element arithmetic
+    one token; T = 16, 64 and 128: tiles that end exactly on a 16-token column
+    group) give the same output bit for bit (the same per-element arithmetic
     in every 16-token group and either shape), within the tolerance of the
     oracle's."""
     nw, rt, b = C.layer_small_tensors(C.WEIGHT_SEED)
